@@ -1,0 +1,114 @@
+/* strata_gfx950: the expert dequant-matmul path of strata-mlx, for AMD MI355X (gfx950).
+ *
+ * Activations multiply weights still packed in the GGUF file's own block formats. A block type is
+ * given by its GGUF type id (strata_mlx/gguf.py:25-33): Q4_0 2, Q5_0 6, Q8_0 8, Q3_K 11, Q4_K 12,
+ * Q6_K 14, IQ3_XXS 18, IQ4_NL 20, IQ3_S 21, IQ4_XS 23, Q2_0 42. A stack of matrices is laid out as
+ * the file lays it out: row r of matrix e starts at byte (e * rows + r) * row_bytes, where
+ * row_bytes = cols / weights_per_block * bytes_per_block.
+ *
+ * Every pointer except `row_ids` of strata_dense_matvec is a device pointer, and every call only
+ * enqueues work on `stream` (a hipStream_t; NULL is the default stream). The library allocates
+ * nothing and never waits for the device. The caller owns all memory: inputs are only read and
+ * outputs are fully written. Calls are reentrant across host threads and streams.
+ * Activation/output dtypes: STRATA_F32, STRATA_F16, STRATA_BF16. Sums are float32 throughout.
+ *
+ * Each entry point returns STRATA_OK (0) or a negative STRATA_ERR_* code: the Python layer raises
+ * ValueError for KIND / SHAPE / DTYPE / ARG, as the reference does for a type or shape its kernels
+ * do not take (strata_mlx/blocks.py:294-295, dense.py:118-119), and RuntimeError for LAUNCH.
+ */
+#ifndef STRATA_GFX950_H
+#define STRATA_GFX950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { STRATA_F32 = 0, STRATA_F16 = 1, STRATA_BF16 = 2 };
+enum {
+  STRATA_OK = 0,
+  STRATA_ERR_KIND = -1,   /* a block type the kernels do not decode */
+  STRATA_ERR_SHAPE = -2,  /* rows of cols weights do not end on a block, or a size out of range */
+  STRATA_ERR_DTYPE = -3,  /* an activation/output dtype the call does not take */
+  STRATA_ERR_LAUNCH = -4, /* the HIP launch failed */
+  STRATA_ERR_ARG = -5     /* a null pointer or a count out of range */
+};
+
+/* ABI version of this header. */
+int strata_abi_version(void);
+
+/* Weights and bytes per block of `kind`; STRATA_ERR_KIND if the kernels do not decode it.
+ * Replaces the BLOCK table, strata_mlx/blocks.py:36-38. */
+int strata_block_info(int kind, int* per_block, int* block_bytes);
+
+/* out[m, r, c] = the weight (m, r, c) of `n_mats` matrices of rows x cols, as float32/16 (bit-exact:
+ * each weight is computed exactly in float32 and rounded once to out_dtype).
+ * Replaces dequantize + _DEQUANT, strata_mlx/blocks.py:515-522, 261-270. */
+int strata_dequant(int kind, const void* blocks, int64_t n_mats, int64_t rows, int64_t cols, void* out,
+                   int out_dtype, void* stream);
+
+/* out[p, r] = W[idx[p], r, :] . x[p / share, :] for p < pairs, W a stack of `experts` matrices of
+ * rows x cols; out (pairs, rows) in x's dtype. Pairs that name the same expert read its bytes once.
+ * idx values must be < experts. Replaces BlockSwitchLinear.__call__ + _MATVEC,
+ * strata_mlx/blocks.py:538-554, 196-220. */
+int strata_expert_matvec(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                         const uint32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share,
+                         void* out, void* stream);
+
+/* strata_expert_matvec over two stacks of one shape that read the same x (gate and up), one launch.
+ * Replaces the gate and up calls of switch_glu, strata_mlx/blocks.py:969. */
+int strata_expert_matvec2(int kind, const void* blocks_a, const void* blocks_b, int64_t experts, int64_t rows,
+                          int64_t cols, const uint32_t* idx, int64_t pairs, const void* x, int x_dtype,
+                          int64_t share, void* out_a, void* out_b, void* stream);
+
+/* out[p, r] = W[idx[p], r, :] . swiglu(gate[p], up[p]) with the SwiGLU rounded as mlx-lm rounds it
+ * (sigmoid in float32 rounded to the activation dtype, then two products in that dtype); gate, up
+ * (pairs, cols). Replaces matvec_glu + _MATVEC_GLU, strata_mlx/blocks.py:939-955, 225-259. */
+int strata_expert_matvec_swiglu(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                                const uint32_t* idx, int64_t pairs, const void* gate, const void* up,
+                                int act_dtype, void* out, void* stream);
+
+/* out[p, r] = E_p[r, :] . x[p / share, :] where per_pair[p] (a device array of device pointers) is
+ * pair p's own rows x cols matrix. Replaces matvec_separate, strata_mlx/blocks.py:331-346. */
+int strata_expert_matvec_ptrs(int kind, const void* const* per_pair, int64_t rows, int64_t cols, int64_t pairs,
+                              const void* x, int x_dtype, int64_t share, void* out, void* stream);
+
+/* out[t, j] = W[row(j), :] . x[t, :] for one matrix W (rows x cols) and `tokens` rows of x; row(j) =
+ * row_ids[j] for j < n_ids when row_ids is given (a device array), else j < rows. out (tokens, n)
+ * in out_dtype. A token gets the same bits whatever the number of tokens with it.
+ * Replaces window_matvec (strata_mlx/blocks.py:383-394), ScaledLinear on Q6_K blocks
+ * (strata_mlx/dense.py:141-167), BlockLinear (dense.py:224-242) and _rows_of (strata_mlx/rows.py:30-42). */
+int strata_dense_matvec(int kind, const void* blocks, int64_t rows, int64_t cols, const void* x, int64_t tokens,
+                        int x_dtype, void* out, int out_dtype, const uint32_t* row_ids, int64_t n_ids,
+                        void* stream);
+
+/* Tiles a prompt's pairs can need at most: pairs / tile + min(experts, pairs). */
+int64_t strata_route_tiles_max(int64_t pairs, int64_t experts, int64_t tile);
+
+/* The pairs idx (tokens x k, flattened) laid out in tiles of `tile` slots, each tile one expert's,
+ * on the device with no host wait: tile_expert[n_tiles] (`experts` for a tile nothing fills),
+ * token[n_tiles * tile] (0 for an empty slot), where[pairs] (the slot of each pair) and, if not
+ * NULL, slot_pair[n_tiles * tile] (the pair of each slot, 0xffffffff for an empty one), with
+ * n_tiles = strata_route_tiles_max(pairs, experts, tile). Slots of an expert go in pair order. A pair
+ * naming no expert (>= experts) gets no slot: its `where` is 0xffffffff. `workspace` is device memory of
+ * strata_route_tiles_workspace(pairs, experts) bytes. Replaces tiles_of, strata_mlx/blocks.py:657-681. */
+int64_t strata_route_tiles_workspace(int64_t pairs, int64_t experts);
+int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t experts, int64_t tile,
+                       uint32_t* tile_expert, uint32_t* token, uint32_t* where, uint32_t* slot_pair,
+                       void* workspace, void* stream);
+
+/* c[s, :] = W[tile_expert[s / tile]] . a[s, :] for s < n_tiles * tile; a (n_tiles * tile, cols) in
+ * a_dtype, c (n_tiles * tile, rows) float32. Tiles naming no expert (>= experts) are skipped and
+ * their rows of c are left as they were. F16/BF16 activations multiply weights rounded to float16
+ * on MFMA (float32 sums); F32 activations multiply exact weights in float32.
+ * Replaces tile_matmul + _TILES, strata_mlx/blocks.py:634-654, 583-626. */
+int strata_grouped_matmul(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                          const void* a, int a_dtype, const uint32_t* tile_expert, int64_t n_tiles, int64_t tile,
+                          float* c, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRATA_GFX950_H */

@@ -1,0 +1,13 @@
+"""strata_mlx_amd: strata-mlx's expert dequant-matmul path, rebuilt for AMD MI355X (gfx950).
+
+Activations multiply weights still packed in the GGUF file's block formats, through hand-written HIP
+kernels behind a C ABI (include/strata_gfx950.h, libstrata_gfx950.so). The Python modules mirror the
+reference's call surface with torch tensors on the GPU:
+
+    blocks   BlockSwitchLinear, BlockSwitchGLU, dequantize, window_matvec, matvec_glu, matvec_separate,
+             tiles_of, tile_matmul, switch_glu            (strata_mlx/blocks.py)
+    dense    ScaledLinear, BlockLinear, BlockEmbedding    (strata_mlx/dense.py)
+    rows     GuessRows row layers on listed lm_head rows (strata_mlx/rows.py)
+"""
+
+__all__ = ["blocks"]

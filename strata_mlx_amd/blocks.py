@@ -1,0 +1,214 @@
+"""Experts computed on the GGUF file's own blocks, on gfx950: the call surface of strata_mlx/blocks.py.
+
+The blocks go to the GPU as the file's bytes (a uint8 tensor) and hand-written HIP kernels read them:
+
+    matvec     out[pair, row] = W[expert of pair, row, :] . x     decode: bandwidth-bound, no MFMA
+               (also with every pair's expert as an array of its own: matvec_separate)
+    window     the same for one layer and a window of tokens (window_matvec, dense.BlockLinear)
+    tiles      a prompt's pairs sorted by expert into tiles; weights decoded into LDS, MFMA products
+    dequant    every weight of the stack as float16 or float32, bit-exact
+
+Sums are float32 whatever the type of the activations. Arguments mirror the reference's, with torch
+tensors on the GPU in place of mx.array.
+"""
+
+import torch
+
+from . import _lib
+
+# type -> (weights per block, bytes per block); strata_mlx/blocks.py:36-38
+BLOCK = {"IQ4_NL": (32, 18), "IQ4_XS": (256, 136), "IQ3_S": (256, 110), "IQ3_XXS": (256, 98),
+         "IQ2_S": (256, 82), "IQ2_XS": (256, 74), "IQ2_XXS": (256, 66), "IQ1_M": (256, 56), "Q2_0": (64, 18),
+         "Q3_K": (256, 110)}
+# the dense types of the loader, decoded by the same kernels (strata_mlx/gguf.py:25-33)
+DENSE = {"Q4_0": (32, 18), "Q5_0": (32, 22), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210)}
+# the codebooks of these were not available to this build: the kernels refuse them
+NO_GRID = ("IQ2_S", "IQ2_XS", "IQ2_XXS", "IQ1_M")
+
+TOKENS_TILE = 16  # slots of a tile (strata_mlx/blocks.py:581)
+TILES_FROM = 1600  # (token, expert) pairs from which a prompt goes through tiles (strata_mlx/blocks.py:580)
+MATVEC_GLU_UPTO = 1 << 16  # pairs for which down takes silu(gate) * up itself (the reference: 30)
+
+
+def row_bytes(kind: str, cols: int) -> int:
+    per_block, block_bytes = {**BLOCK, **DENSE}[kind]
+    if cols % per_block:
+        raise ValueError(f"{kind}: rows of {cols} weights do not end on a block of {per_block}")
+    return cols // per_block * block_bytes
+
+
+def _flat_u8(blocks: torch.Tensor) -> torch.Tensor:
+    if blocks.dtype != torch.uint8:
+        raise ValueError("blocks must be the file's bytes, uint8")
+    _lib.require_device(blocks)
+    return blocks
+
+
+def dequantize(blocks: torch.Tensor, kind: str, shape: tuple, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """The weights of `blocks` (uint8, a tensor of `shape` as the file holds it) as floats, bit-exact.
+    strata_mlx/blocks.py:515-522."""
+    *lead, rows, cols = shape
+    n = 1
+    for v in lead:
+        n *= v
+    _flat_u8(blocks)
+    if blocks.numel() < n * rows * row_bytes(kind, cols):
+        raise ValueError("blocks hold fewer bytes than the shape needs")
+    out = torch.empty(tuple(shape), dtype=dtype, device=blocks.device)
+    if dtype not in (torch.float32, torch.float16):
+        raise ValueError("dequantize gives float32 or float16")
+    _lib.check(_lib.library().strata_dequant(_lib.kind_id(kind), blocks.data_ptr(), n, rows, cols, out.data_ptr(),
+                                             _lib.dtype_id(dtype), _lib.stream()), f"dequantize {kind}")
+    return out
+
+
+def _idx32(indices: torch.Tensor) -> torch.Tensor:
+    return indices.reshape(-1).to(torch.int32).contiguous()
+
+
+class BlockSwitchLinear:
+    """A stack of linear layers kept as the file's blocks; called like mlx-lm's `QuantizedSwitchLinear`.
+    strata_mlx/blocks.py:525-558."""
+
+    unpack_from = 5000  # pairs from which the reference multiplies unpacked floats; here a kernel either way
+
+    def __init__(self, blocks: torch.Tensor, kind: str, shape: tuple, per_row: int | None = None):
+        self.blocks, self.kind = _flat_u8(blocks), kind
+        self.num_experts, self.output_dims, self.input_dims = shape
+        self.row_bytes = row_bytes(kind, self.input_dims)
+        if blocks.numel() < self.num_experts * self.output_dims * self.row_bytes:
+            raise ValueError("blocks hold fewer bytes than the shape needs")
+        self.per_row = per_row  # accepted for the reference's signature; the kernel sets its own split
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor, sorted_indices: bool = False) -> torch.Tensor:
+        """x (..., 1, in), one row to each index or to each run of the last axis of `indices`."""
+        indices = torch.as_tensor(indices, device=x.device)
+        batch, k = tuple(x.shape[:-2]), (indices.shape[-1] if indices.ndim else 1)
+        ishape = tuple(indices.shape)
+        if batch == ishape:
+            share = 1
+        elif batch == (*ishape[:-1], 1):
+            share = k
+        else:
+            x, share = x.expand(*ishape, 1, self.input_dims), 1
+        pairs = indices.numel()
+        x2 = x.reshape(-1, self.input_dims).contiguous()
+        out = torch.empty((pairs, self.output_dims), dtype=x.dtype, device=x.device)
+        idx = _idx32(indices)
+        _lib.check(_lib.library().strata_expert_matvec(
+            _lib.kind_id(self.kind), self.blocks.data_ptr(), self.num_experts, self.output_dims, self.input_dims,
+            idx.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), share, out.data_ptr(), _lib.stream()),
+            f"matvec {self.kind}")
+        return out.reshape(*ishape, 1, self.output_dims)
+
+
+def gate_up(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tensor, idx: torch.Tensor, share: int):
+    """(gate . x, up . x) for every pair in one launch; x (pairs / share, in), idx (pairs,) -> two (pairs, out)."""
+    if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) != (up.kind, up.output_dims, up.input_dims,
+                                                                             up.num_experts):
+        raise ValueError("gate and up differ in type or shape")
+    pairs = idx.numel()
+    x2 = x.reshape(-1, gate.input_dims).contiguous()
+    g = torch.empty((pairs, gate.output_dims), dtype=x.dtype, device=x.device)
+    u = torch.empty_like(g)
+    idx = _idx32(idx)
+    _lib.check(_lib.library().strata_expert_matvec2(
+        _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), gate.num_experts, gate.output_dims,
+        gate.input_dims, idx.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), share, g.data_ptr(),
+        u.data_ptr(), _lib.stream()), f"gate/up {gate.kind}")
+    return g, u
+
+
+def matvec_glu(lin: BlockSwitchLinear, idx: torch.Tensor, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """`lin(swiglu(gate, up), idx)`, one pair to each row of gate and up: (pairs, out). The SwiGLU is rounded as
+    mlx-lm rounds it. strata_mlx/blocks.py:939-955."""
+    pairs = idx.numel()
+    gate, up = gate.reshape(pairs, -1).contiguous(), up.reshape(pairs, -1).contiguous()
+    out = torch.empty((pairs, lin.output_dims), dtype=gate.dtype, device=gate.device)
+    idx = _idx32(idx)
+    _lib.check(_lib.library().strata_expert_matvec_swiglu(
+        _lib.kind_id(lin.kind), lin.blocks.data_ptr(), lin.num_experts, lin.output_dims, lin.input_dims,
+        idx.data_ptr(), pairs, gate.data_ptr(), up.data_ptr(), _lib.dtype_id(gate.dtype), out.data_ptr(),
+        _lib.stream()), f"matvec_glu {lin.kind}")
+    return out
+
+
+def matvec_separate(experts: list, kind: str, rows: int, cols: int, x: torch.Tensor, share: int) -> torch.Tensor:
+    """out[pair] = W[pair] . x, every pair bringing its expert's blocks as a tensor of its own.
+    x (pairs / share, cols). Returns (pairs, rows). strata_mlx/blocks.py:331-346."""
+    n = len(experts)
+    for e in experts:
+        _flat_u8(e)
+    ptrs = torch.tensor([e.data_ptr() for e in experts], dtype=torch.int64, device=x.device)
+    x2 = x.reshape(-1, cols).contiguous()
+    out = torch.empty((n, rows), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.library().strata_expert_matvec_ptrs(
+        _lib.kind_id(kind), ptrs.data_ptr(), rows, cols, n, x2.data_ptr(), _lib.dtype_id(x.dtype), share,
+        out.data_ptr(), _lib.stream()), f"matvec_separate {kind}")
+    return out
+
+
+def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor,
+                  per_row: int | None = None, row_ids: torch.Tensor | None = None,
+                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """out[t] = W . x[t] for one layer `blocks` of (rows, cols) and x (tokens, cols): (tokens, rows), or
+    (tokens, len(row_ids)) over the listed rows only. strata_mlx/blocks.py:383-394."""
+    _flat_u8(blocks)
+    x2 = x.reshape(-1, cols).contiguous()
+    tokens = x2.shape[0]
+    n = rows if row_ids is None else row_ids.numel()
+    out_dtype = out_dtype or x.dtype
+    out = torch.empty((tokens, n), dtype=out_dtype, device=x.device)
+    ids = None if row_ids is None else row_ids.reshape(-1).to(torch.int32).contiguous()
+    _lib.check(_lib.library().strata_dense_matvec(
+        _lib.kind_id(kind), blocks.data_ptr(), rows, cols, x2.data_ptr(), tokens, _lib.dtype_id(x.dtype),
+        out.data_ptr(), _lib.dtype_id(out_dtype), _lib.ptr(ids), n if ids is not None else 0, _lib.stream()),
+        f"window {kind}")
+    return out
+
+
+def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, gate: BlockSwitchLinear,
+               down: BlockSwitchLinear) -> torch.Tensor:
+    """down(silu(gate(x)) * up(x)) through each token's experts: x (..., in), indices (..., k) -> (..., k, out).
+    The argument order is the reference's (x, indices, up, gate, down); strata_mlx/blocks.py:958-986.
+
+    Decode windows take the matvec kernels: gate and up in one launch reading x once, then down with the SwiGLU
+    worked out in its own registers, rounded as mlx-lm rounds it. Prompt chunks (from TILES_FROM pairs) take the
+    tiles: the pairs sorted by expert on the GPU, weights decoded into LDS and multiplied on MFMA."""
+    indices = torch.as_tensor(indices, device=x.device)
+    k = indices.shape[-1] if indices.ndim else 1
+    flat = indices.reshape(-1)
+    xs = x.reshape(-1, x.shape[-1])
+    if flat.numel() >= TILES_FROM and all(tileable(lin.kind, lin.output_dims, lin.input_dims)
+                                          for lin in (up, gate, down)):
+        return _tiled_glu(x, indices, up, gate, down)
+    if (gate.kind, gate.output_dims, gate.input_dims) == (up.kind, up.output_dims, up.input_dims):
+        g, u = gate_up(gate, up, xs, flat, k)
+    else:
+        g = gate(xs.reshape(-1, 1, 1, xs.shape[-1]).expand(-1, 1, 1, -1), indices.reshape(-1, k)).reshape(flat.numel(), -1)
+        u = up(xs.reshape(-1, 1, 1, xs.shape[-1]).expand(-1, 1, 1, -1), indices.reshape(-1, k)).reshape(flat.numel(), -1)
+    out = matvec_glu(down, flat, g, u)
+    return out.reshape(*indices.shape, down.output_dims)
+
+
+class BlockSwitchGLU:
+    """A layer's routed experts, called like mlx-lm's `SwitchGLU`; strata_mlx/blocks.py:989-996."""
+
+    def __init__(self, gate: BlockSwitchLinear, up: BlockSwitchLinear, down: BlockSwitchLinear):
+        self.gate_proj, self.up_proj, self.down_proj = gate, up, down
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        return switch_glu(x, indices, self.up_proj, self.gate_proj, self.down_proj)
+
+
+ROWS_TILE, COLS_TILE = 64, 64  # what a tile takes (strata_mlx/blocks.py:581, 629-631)
+
+
+def tileable(kind: str, rows: int, cols: int) -> bool:
+    """Whether `tile_matmul` takes a stack of such layers; strata_mlx/blocks.py:629-631."""
+    per_block = {**BLOCK, **DENSE}[kind][0]
+    return rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % per_block == 0 and kind not in NO_GRID
+
+
+def _tiled_glu(x, indices, up, gate, down):
+    raise NotImplementedError  # filled in by the tiles section below

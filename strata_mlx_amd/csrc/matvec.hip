@@ -1,0 +1,205 @@
+// C-ABI entry points of the dequant and matvec family (declared in include/strata_gfx950.h).
+// Arguments are checked here; the kernels live in matvec_impl.h, one object per block type.
+#include "matvec_impl.h"
+
+namespace strata_mv {
+#define STRATA_DECLARE(K)                                                                                    \
+  int matvec_launch_##K(MatvecParams&, int, int, bool, int, int, hipStream_t);                              \
+  int dequant_launch_##K(const uint8_t*, int64_t, int, int, void*, int, hipStream_t);
+STRATA_DECLARE(2)
+STRATA_DECLARE(6)
+STRATA_DECLARE(8)
+STRATA_DECLARE(11)
+STRATA_DECLARE(12)
+STRATA_DECLARE(14)
+STRATA_DECLARE(18)
+STRATA_DECLARE(20)
+STRATA_DECLARE(21)
+STRATA_DECLARE(23)
+STRATA_DECLARE(42)
+#undef STRATA_DECLARE
+}  // namespace strata_mv
+
+using namespace strata_mv;
+
+namespace {
+
+int launch_by_kind(int kind, MatvecParams& p, int x_dtype, int out_dtype, bool glu, int gy, int gz, hipStream_t s) {
+  switch (kind) {
+#define STRATA_CASE(K) \
+  case K: return matvec_launch_##K(p, x_dtype, out_dtype, glu, gy, gz, s);
+    STRATA_CASE(2)
+    STRATA_CASE(6)
+    STRATA_CASE(8)
+    STRATA_CASE(11)
+    STRATA_CASE(12)
+    STRATA_CASE(14)
+    STRATA_CASE(18)
+    STRATA_CASE(20)
+    STRATA_CASE(21)
+    STRATA_CASE(23)
+    STRATA_CASE(42)
+#undef STRATA_CASE
+    default: return STRATA_ERR_KIND;
+  }
+}
+
+int dequant_by_kind(int kind, const uint8_t* b, int64_t runs, int per_row, int row_bytes, void* out, int dt,
+                    hipStream_t s) {
+  switch (kind) {
+#define STRATA_CASE(K) \
+  case K: return dequant_launch_##K(b, runs, per_row, row_bytes, out, dt, s);
+    STRATA_CASE(2)
+    STRATA_CASE(6)
+    STRATA_CASE(8)
+    STRATA_CASE(11)
+    STRATA_CASE(12)
+    STRATA_CASE(14)
+    STRATA_CASE(18)
+    STRATA_CASE(20)
+    STRATA_CASE(21)
+    STRATA_CASE(23)
+    STRATA_CASE(42)
+#undef STRATA_CASE
+    default: return STRATA_ERR_KIND;
+  }
+}
+
+int block_shape(int kind, int64_t rows, int64_t cols, int* row_bytes) {
+  int per = 0, bb = 0;
+  if (strata_kind_info(kind, &per, &bb)) return STRATA_ERR_KIND;
+  if (rows < 0 || cols <= 0 || cols % per || cols % 32) return STRATA_ERR_SHAPE;
+  if (rows > (1 << 30) || cols > (1 << 20)) return STRATA_ERR_SHAPE;
+  *row_bytes = (int)(cols / per * bb);
+  return STRATA_OK;
+}
+
+bool valid_dtype(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
+
+int expert_common(int kind, const void* a, const void* b, int64_t experts, int64_t rows, int64_t cols,
+                  const uint32_t* idx, int64_t pairs, const void* x, const void* up, int dtype, int64_t share,
+                  void* out_a, void* out_b, bool glu, void* stream) {
+  MatvecParams p = {};
+  int rc = block_shape(kind, rows, cols, &p.row_bytes);
+  if (rc) return rc;
+  if (!valid_dtype(dtype)) return STRATA_ERR_DTYPE;
+  if (pairs < 0 || experts < 0 || experts > INT32_MAX) return STRATA_ERR_ARG;
+  if (pairs == 0 || rows == 0) return STRATA_OK;
+  if (!a || !idx || !x || !out_a || (b && !out_b) || (glu && !up)) return STRATA_ERR_ARG;
+  if (share < 1 || pairs % share) return STRATA_ERR_ARG;
+  if (pairs > 65535 || cols / 32 > 256) return STRATA_ERR_SHAPE;
+  p.blocks[0] = (const uint8_t*)a;
+  p.blocks[1] = (const uint8_t*)b;
+  p.out[0] = out_a;
+  p.out[1] = out_b;
+  p.idx = idx;
+  p.x = x;
+  p.up = up;
+  p.mat_bytes = rows * (int64_t)p.row_bytes;
+  p.experts = experts;
+  p.src_rows = (int)rows;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.pairs = (int)pairs;
+  p.share = (int)share;
+  p.mode = MODE_EXPERT;
+  return launch_by_kind(kind, p, dtype, dtype, glu, (int)pairs, b ? 2 : 1, (hipStream_t)stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int strata_abi_version(void) { return 1; }
+
+int strata_block_info(int kind, int* per_block, int* block_bytes) {
+  return strata_kind_info(kind, per_block, block_bytes) ? STRATA_ERR_KIND : STRATA_OK;
+}
+
+int strata_dequant(int kind, const void* blocks, int64_t n_mats, int64_t rows, int64_t cols, void* out,
+                   int out_dtype, void* stream) {
+  int row_bytes = 0;
+  int rc = block_shape(kind, rows, cols, &row_bytes);
+  if (rc) return rc;
+  if (n_mats < 0) return STRATA_ERR_SHAPE;
+  if (out_dtype != DT_F32 && out_dtype != DT_F16) return STRATA_ERR_DTYPE;
+  const int64_t runs_total = n_mats * rows * (cols / 32);
+  if (runs_total == 0) return STRATA_OK;
+  if (!blocks || !out) return STRATA_ERR_ARG;
+  if ((runs_total + 255) / 256 > INT32_MAX) return STRATA_ERR_SHAPE;
+  return dequant_by_kind(kind, (const uint8_t*)blocks, runs_total, (int)(cols / 32), row_bytes, out, out_dtype,
+                         (hipStream_t)stream);
+}
+
+int strata_expert_matvec(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                         const uint32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share, void* out,
+                         void* stream) {
+  return expert_common(kind, blocks, nullptr, experts, rows, cols, idx, pairs, x, nullptr, x_dtype, share, out,
+                       nullptr, false, stream);
+}
+
+int strata_expert_matvec2(int kind, const void* blocks_a, const void* blocks_b, int64_t experts, int64_t rows,
+                          int64_t cols, const uint32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share,
+                          void* out_a, void* out_b, void* stream) {
+  if (!blocks_b && pairs > 0 && rows > 0) return STRATA_ERR_ARG;
+  return expert_common(kind, blocks_a, blocks_b, experts, rows, cols, idx, pairs, x, nullptr, x_dtype, share, out_a,
+                       out_b, false, stream);
+}
+
+int strata_expert_matvec_swiglu(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                                const uint32_t* idx, int64_t pairs, const void* gate, const void* up, int act_dtype,
+                                void* out, void* stream) {
+  return expert_common(kind, blocks, nullptr, experts, rows, cols, idx, pairs, gate, up, act_dtype, 1, out, nullptr,
+                       true, stream);
+}
+
+int strata_expert_matvec_ptrs(int kind, const void* const* per_pair, int64_t rows, int64_t cols, int64_t pairs,
+                              const void* x, int x_dtype, int64_t share, void* out, void* stream) {
+  MatvecParams p = {};
+  int rc = block_shape(kind, rows, cols, &p.row_bytes);
+  if (rc) return rc;
+  if (!valid_dtype(x_dtype)) return STRATA_ERR_DTYPE;
+  if (pairs < 0) return STRATA_ERR_ARG;
+  if (pairs == 0 || rows == 0) return STRATA_OK;
+  if (!per_pair || !x || !out) return STRATA_ERR_ARG;
+  if (share < 1 || pairs % share) return STRATA_ERR_ARG;
+  if (pairs > 65535 || cols / 32 > 256) return STRATA_ERR_SHAPE;
+  p.ptrs = (const uint8_t* const*)per_pair;
+  p.out[0] = out;
+  p.x = x;
+  p.mat_bytes = rows * (int64_t)p.row_bytes;
+  p.src_rows = (int)rows;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.pairs = (int)pairs;
+  p.share = (int)share;
+  p.mode = MODE_PTRS;
+  return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 1, (hipStream_t)stream);
+}
+
+int strata_dense_matvec(int kind, const void* blocks, int64_t rows, int64_t cols, const void* x, int64_t tokens,
+                        int x_dtype, void* out, int out_dtype, const uint32_t* row_ids, int64_t n_ids, void* stream) {
+  MatvecParams p = {};
+  int rc = block_shape(kind, rows, cols, &p.row_bytes);
+  if (rc) return rc;
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return STRATA_ERR_DTYPE;
+  if (tokens < 0 || (row_ids && n_ids < 0)) return STRATA_ERR_ARG;
+  const int64_t out_rows = row_ids ? n_ids : rows;
+  if (tokens == 0 || out_rows == 0) return STRATA_OK;
+  if (!blocks || !x || !out) return STRATA_ERR_ARG;
+  if (tokens > 65535 || out_rows > INT32_MAX / 2 || cols / 32 > 256) return STRATA_ERR_SHAPE;
+  if (out_dtype != x_dtype && out_dtype != DT_F32) return STRATA_ERR_DTYPE;
+  p.blocks[0] = (const uint8_t*)blocks;
+  p.out[0] = out;
+  p.row_ids = row_ids;
+  p.x = x;
+  p.mat_bytes = rows * (int64_t)p.row_bytes;
+  p.src_rows = (int)rows;
+  p.rows = (int)out_rows;
+  p.cols = (int)cols;
+  p.tokens = (int)tokens;
+  p.mode = MODE_DENSE;
+  return launch_by_kind(kind, p, x_dtype, out_dtype, false, 1, 1, (hipStream_t)stream);
+}
+
+}  // extern "C"

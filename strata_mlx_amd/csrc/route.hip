@@ -1,0 +1,151 @@
+// A prompt's (token, expert) pairs laid out in tiles of `tile` slots, each tile one expert's, on the GPU.
+//
+// The reference works this out with MLX operations on the GPU so the host never waits for the router
+// (strata_mlx/blocks.py:657-681): an argsort by expert, per-expert counts, cumulative sums and scatters.
+// Here it is a counting sort in three kernels over blocks of 256 pairs, stable so that an expert's slots
+// go in pair order:
+//   count  each block counts its pairs per expert                       blk[b][e]
+//   scan   per expert, the blocks' exclusive prefix (blk becomes offsets); per-expert tiles, their
+//          prefix over experts (the expert's first tile), tile_expert, and every slot made empty
+//   place  each pair's rank among its block's pairs of the same expert (wave ballots, then the waves
+//          before it), plus its block's offset: the slot; where, token and slot_pair written
+// The tile count is pairs / tile + min(experts, pairs) whatever the routing, as the reference's.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;  // pairs per block of the count and place kernels
+constexpr uint32_t kNone = 0xffffffffu;
+
+__global__ __launch_bounds__(kBlock) void route_count(const uint32_t* idx, int pairs, int experts, uint32_t* blk) {
+  extern __shared__ uint32_t cnt[];  // [experts]
+  for (int e = threadIdx.x; e < experts; e += kBlock) cnt[e] = 0;
+  __syncthreads();
+  const int p = blockIdx.x * kBlock + threadIdx.x;
+  if (p < pairs) {
+    const uint32_t e = idx[p];
+    if (e < (uint32_t)experts) atomicAdd(&cnt[e], 1u);
+  }
+  __syncthreads();
+  uint32_t* row = blk + (int64_t)blockIdx.x * experts;
+  for (int e = threadIdx.x; e < experts; e += kBlock) row[e] = cnt[e];
+}
+
+// One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void route_scan(uint32_t* blk, int nblocks, int experts, int tile, int n_tiles,
+                                                  uint32_t* first_tile, uint32_t* tile_expert, uint32_t* token,
+                                                  uint32_t* slot_pair) {
+  extern __shared__ uint32_t sh[];  // tiles per expert, then their scan: [experts + 1]
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int e = tid; e < experts; e += nt) {
+    uint32_t run = 0;
+    for (int b = 0; b < nblocks; ++b) {
+      const uint32_t v = blk[(int64_t)b * experts + e];
+      blk[(int64_t)b * experts + e] = run;
+      run += v;
+    }
+    sh[e] = (run + tile - 1) / tile;
+  }
+  __syncthreads();
+  if (tid == 0) {  // exclusive scan of the tile counts; experts <= 65536, a few microseconds at most
+    uint32_t run = 0;
+    for (int e = 0; e < experts; ++e) {
+      const uint32_t v = sh[e];
+      sh[e] = run;
+      run += v;
+    }
+    sh[experts] = run;
+  }
+  __syncthreads();
+  for (int e = tid; e < experts; e += nt) {
+    first_tile[e] = sh[e];
+    for (uint32_t t = sh[e]; t < sh[e + 1]; ++t) tile_expert[t] = (uint32_t)e;
+  }
+  for (int t = (int)sh[experts] + tid; t < n_tiles; t += nt) tile_expert[t] = (uint32_t)experts;
+  const int64_t slots = (int64_t)n_tiles * tile;
+  for (int64_t s = tid; s < slots; s += nt) {
+    token[s] = 0;
+    if (slot_pair) slot_pair[s] = kNone;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void route_place(const uint32_t* idx, int pairs, int k, int experts, int tile,
+                                                      const uint32_t* blk, const uint32_t* first_tile,
+                                                      uint32_t* token, uint32_t* where, uint32_t* slot_pair) {
+  extern __shared__ uint32_t wcnt[];  // [4 waves][experts]: pairs of each expert in each wave
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  for (int i = tid; i < 4 * experts; i += kBlock) wcnt[i] = 0;
+  __syncthreads();
+  const int p = blockIdx.x * kBlock + tid;
+  const bool valid = p < pairs && idx[p] < (uint32_t)experts;
+  const uint32_t e = valid ? idx[p] : kNone;
+  // the lanes of this wave with the same expert: one ballot per distinct expert in the wave
+  uint64_t remaining = __ballot(valid);
+  uint64_t mine = 0;
+  while (remaining) {
+    const int leader = __ffsll((unsigned long long)remaining) - 1;
+    const uint32_t le = __shfl(e, leader);
+    const uint64_t same = __ballot(valid && e == le);
+    if (valid && e == le) mine = same;
+    if (lane == leader) wcnt[wave * experts + le] = (uint32_t)__popcll(same);
+    remaining &= ~same;
+  }
+  __syncthreads();
+  if (p < pairs) {
+    if (!valid) {
+      where[p] = kNone;
+      return;
+    }
+    uint32_t rank = blk[(int64_t)blockIdx.x * experts + e] + (uint32_t)__popcll(mine & ((1ull << lane) - 1));
+    for (int w = 0; w < wave; ++w) rank += wcnt[w * experts + e];
+    const uint32_t slot = first_tile[e] * tile + rank;
+    where[p] = slot;
+    token[slot] = (uint32_t)(p / k);
+    if (slot_pair) slot_pair[slot] = (uint32_t)p;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t strata_route_tiles_max(int64_t pairs, int64_t experts, int64_t tile) {
+  if (pairs < 0 || experts < 0 || tile <= 0) return 0;
+  return pairs / tile + (experts < pairs ? experts : pairs);
+}
+
+int64_t strata_route_tiles_workspace(int64_t pairs, int64_t experts) {
+  if (pairs < 0 || experts < 0) return 0;
+  const int64_t nblocks = (pairs + kBlock - 1) / kBlock;
+  return (nblocks * experts + experts + 64) * (int64_t)sizeof(uint32_t);
+}
+
+int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t experts, int64_t tile,
+                       uint32_t* tile_expert, uint32_t* token, uint32_t* where, uint32_t* slot_pair, void* workspace,
+                       void* stream) {
+  if (pairs < 0 || k < 1 || experts < 1 || tile < 1 || tile > 1024) return STRATA_ERR_ARG;
+  if (experts > 2048 || pairs > (1 << 24)) return STRATA_ERR_SHAPE;  // the place kernel holds 4 x experts counts in LDS
+  const int64_t n_tiles = strata_route_tiles_max(pairs, experts, tile);
+  if (n_tiles == 0) return STRATA_OK;
+  if (!tile_expert || !token || !workspace || (pairs > 0 && (!idx || !where))) return STRATA_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const int nblocks = (int)((pairs + kBlock - 1) / kBlock);
+  uint32_t* blk = (uint32_t*)workspace;
+  uint32_t* first_tile = blk + (int64_t)nblocks * experts;
+  const size_t lds_e = (size_t)experts * sizeof(uint32_t);
+  if (nblocks > 0) {
+    hipLaunchKernelGGL(route_count, dim3(nblocks), dim3(kBlock), lds_e, s, idx, (int)pairs, (int)experts, blk);
+    STRATA_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(route_scan, dim3(1), dim3(1024), lds_e + sizeof(uint32_t), s, blk, nblocks, (int)experts,
+                     (int)tile, (int)n_tiles, first_tile, tile_expert, token, slot_pair);
+  STRATA_CHECK_LAUNCH();
+  if (nblocks > 0) {
+    hipLaunchKernelGGL(route_place, dim3(nblocks), dim3(kBlock), 4 * lds_e, s, idx, (int)pairs, (int)k, (int)experts,
+                       (int)tile, blk, first_tile, token, where, slot_pair);
+    STRATA_CHECK_LAUNCH();
+  }
+  return STRATA_OK;
+}
+
+}  // extern "C"

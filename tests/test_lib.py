@@ -1,0 +1,63 @@
+"""The C-ABI library loads without a GPU, exports every symbol include/strata_gfx950.h declares, and refuses bad
+arguments before it touches the device (no compute call runs here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from strata_mlx_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "strata_gfx950.h")).read()
+    return re.findall(r"^(?:int|int64_t)\s+(strata_\w+)\(", text, re.M)
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.library()
+    names = declared()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+    assert lib.strata_abi_version() == 1
+
+
+@pytest.mark.parametrize("kind, per, size", [("Q2_0", 64, 18), ("IQ3_S", 256, 110), ("IQ3_XXS", 256, 98),
+                                             ("Q4_K", 256, 144), ("Q6_K", 256, 210), ("Q8_0", 32, 34),
+                                             ("IQ4_NL", 32, 18), ("IQ4_XS", 256, 136), ("Q3_K", 256, 110),
+                                             ("Q4_0", 32, 18), ("Q5_0", 32, 22)])
+def test_block_info(kind, per, size):
+    p, b = ctypes.c_int(), ctypes.c_int()
+    assert _lib.library().strata_block_info(_lib.kind_id(kind), ctypes.byref(p), ctypes.byref(b)) == 0
+    assert (p.value, b.value) == (per, size)
+
+
+@pytest.mark.parametrize("kind", ["IQ2_S", "IQ2_XS", "IQ2_XXS", "IQ1_M", "Q5_K"])
+def test_types_without_kernels_are_refused(kind):
+    lib = _lib.library()
+    assert lib.strata_block_info(_lib.kind_id(kind), None, None) == _lib.ERR_KIND
+    assert lib.strata_dequant(_lib.kind_id(kind), 1, 1, 1, 256, 1, 0, None) == _lib.ERR_KIND
+
+
+def test_arguments_are_checked_before_any_launch():
+    lib = _lib.library()
+    q = _lib.kind_id("IQ3_S")
+    assert lib.strata_dequant(q, 1, 1, 4, 100, 1, 0, None) == _lib.ERR_SHAPE  # 100 is not a block of 256
+    assert lib.strata_dequant(q, 1, 1, 4, 256, 1, 2, None) == _lib.ERR_DTYPE  # bf16 out
+    assert lib.strata_dequant(q, 0, 1, 4, 256, 0, 0, None) == _lib.ERR_ARG  # null pointers
+    assert lib.strata_dequant(q, 0, 0, 4, 256, 0, 0, None) == _lib.OK  # nothing to do
+    assert lib.strata_expert_matvec(q, 1, 4, 8, 256, 1, 6, 1, 1, 4, 1, None) == _lib.ERR_ARG  # 6 pairs, share 4
+    assert lib.strata_expert_matvec(q, 1, 4, 8, 256, 1, 4, 1, 7, 1, 1, None) == _lib.ERR_DTYPE
+    assert lib.strata_expert_matvec(q, 1, 4, 8, 16384, 1, 4, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # > 8192 cols
+    assert lib.strata_expert_matvec(99, 1, 4, 8, 256, 1, 4, 1, 1, 1, 1, None) == _lib.ERR_KIND
+    assert lib.strata_dense_matvec(q, 1, 8, 256, 1, 1, 1, 1, 2, None, 0, None) == _lib.ERR_DTYPE  # f16 -> bf16
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_SHAPE, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_LAUNCH, "x")
