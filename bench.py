@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""Benchmark of the expert dequant-matmul path on one MI355X.
+
+Headline (value): routed-expert decode matvec, IQ3_S, 256 experts top-8 of Zipf(1.1) routing, gate/up 1536 x 4096
+and down 4096 x 1536 with the SwiGLU in down, float16 activations, batch 1. A step is one decode pass of the
+batch through 16 distinct routed-expert layers (about 1 GB of expert bytes, four times the 256 MB MALL), captured
+once as a HIP graph and replayed; each layer is two launches (gate+up, then down with SwiGLU).
+value = algorithmic bytes / time: the distinct experts' packed bytes plus activations in and out.
+
+Beside it, on the same line:
+  decode_t4   the same at 4 tokens (the other batch of the decode workload)
+  prompt      512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, three MFMA
+              grouped products; TFLOPS over the real pairs' 2 * pairs * 3 * 4096 * 1536 flops
+  roofline    the dominant kernel (gate+up matvec): algorithmic bytes per launch / its mean duration (HIP
+              events around a graph of those launches only), against 8 TB/s
+  cpu_baseline the oracle's numpy decode + matvec (the reference's CPU path restated) on a few layers
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+E, H, F, K = 256, 4096, 1536, 8
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prompt", action="store_true")
+    return ap.parse_args()
+
+
+def time_graph(graph, steps, warmup):
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3  # seconds
+
+
+def decode_layers(B, synth, dev, layers):
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    out = []
+    for _ in range(layers):
+        mats = [synth.random_stack("IQ3_S", E * r * c, dev, g) for r, c in ((F, H), (F, H), (H, F))]
+        out.append((B.BlockSwitchLinear(mats[0], "IQ3_S", (E, F, H)), B.BlockSwitchLinear(mats[1], "IQ3_S", (E, F, H)),
+                    B.BlockSwitchLinear(mats[2], "IQ3_S", (E, H, F))))
+    return out
+
+
+def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
+    """Returns (GB/s, ms per step, bytes per step, gate/up launch: (bytes, mean seconds), routes)."""
+    routes = [synth.zipf_routing(tokens, E, K, rng)[0] for _ in lins]
+    idx = [torch.from_numpy(r).to(torch.int32).to(dev) for r in routes]
+    x = (torch.randn((tokens, H), device=dev)).half()
+    mat_bytes = F * H // 256 * 110
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):  # one eager pass first: the library's lazy state, torch's allocator
+        for (gate, up, down), ix in zip(lins, idx):
+            g_, u_ = B.gate_up(gate, up, x, ix, K)
+            B.matvec_glu(down, ix.reshape(-1), g_, u_)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    full, gu = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(full):
+        for (gate, up, down), ix in zip(lins, idx):
+            g_, u_ = B.gate_up(gate, up, x, ix, K)
+            B.matvec_glu(down, ix.reshape(-1), g_, u_)
+    with torch.cuda.graph(gu):
+        for (gate, up, down), ix in zip(lins, idx):
+            B.gate_up(gate, up, x, ix, K)
+    step_bytes, gu_bytes = 0, 0
+    for r in routes:
+        d = len(np.unique(r))
+        act = tokens * H * 2 + 2 * tokens * K * F * 2  # x in; g, u out
+        gu_bytes += d * 2 * mat_bytes + act
+        step_bytes += d * 3 * mat_bytes + act + 2 * tokens * K * F * 2 + tokens * K * H * 2  # g, u in; y out
+    t = time_graph(full, steps, warmup)
+    t_gu = time_graph(gu, steps, warmup)
+    launches = steps * len(lins)
+    return (step_bytes * steps / t / 1e9, t / steps * 1e3, step_bytes, (gu_bytes / len(lins), t_gu / launches),
+            routes)
+
+
+def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512):
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    lins = []
+    for _ in range(layers):
+        mats = [synth.random_stack("IQ3_XXS", E * r * c, dev, g) for r, c in ((F, H), (F, H), (H, F))]
+        lins.append((B.BlockSwitchLinear(mats[0], "IQ3_XXS", (E, F, H)),
+                     B.BlockSwitchLinear(mats[1], "IQ3_XXS", (E, F, H)),
+                     B.BlockSwitchLinear(mats[2], "IQ3_XXS", (E, H, F))))
+    idx = [torch.from_numpy(synth.zipf_routing(tokens, E, K, rng)[0]).to(torch.int32).to(dev) for _ in lins]
+    x = torch.randn((tokens, H), device=dev).to(torch.bfloat16)
+    for (gate, up, down), ix in zip(lins, idx):
+        B._tiled_glu(x, ix, up, gate, down)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for (gate, up, down), ix in zip(lins, idx):
+            B._tiled_glu(x, ix, up, gate, down)
+    t = time_graph(graph, steps, warmup)
+    flops = 2.0 * tokens * K * 3 * H * F * layers
+    tflops = flops * steps / t / 1e12
+    return {"workload": "prompt chunk 512 tokens, IQ3_XXS, 256 experts top-8, bf16", "tflops": round(tflops, 2),
+            "ms_per_layer": round(t / steps / layers * 1e3, 4), "mfma_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "hbm_bound_tflops": round(2.0 * tokens * K * 3 * H * F / (3 * E * F * H / 256 * 98) * HBM_PEAK_GBS / 1e3, 1)}
+
+
+def cpu_baseline(lins, routes, tokens, budget_s=15.0, max_layers=4):
+    """The oracle's numpy decode of the touched experts and their matvecs, one thread, layer by layer until about
+    budget_s of CPU work. The experts' bytes are copied to the host first, untimed: the CPU path reads them from
+    memory. Returns (layers, algorithmic bytes, seconds)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import blocks as O
+
+    mat_bytes = F * H // 256 * 110
+    done, secs, layers = 0, 0.0, 0
+    x = np.random.default_rng(5).standard_normal((tokens, H)).astype(np.float16)
+    with threadpool_limits(limits=1):
+        for (gate, up, down), r in zip(lins, routes):
+            used = [int(e) for e in np.unique(r)]
+            host = {n: {e: lin.blocks[e * mat_bytes:(e + 1) * mat_bytes].cpu().numpy() for e in used}
+                    for n, lin in (("gate", gate), ("up", up), ("down", down))}
+            t0 = time.perf_counter()
+            w = {n: {e: O.dequantize(b, "IQ3_S", (H, F) if n == "down" else (F, H)) for e, b in host[n].items()}
+                 for n in host}
+            flat = r.reshape(-1)
+            g = np.stack([w["gate"][int(e)] @ x[p // K].astype(np.float32) for p, e in enumerate(flat)])
+            u = np.stack([w["up"][int(e)] @ x[p // K].astype(np.float32) for p, e in enumerate(flat)])
+            h = O.swiglu_rounded(g.astype(np.float16), u.astype(np.float16), np.float16)
+            np.stack([w["down"][int(e)] @ h[p].astype(np.float32) for p, e in enumerate(flat)])
+            secs += time.perf_counter() - t0
+            layers += 1
+            done += len(used) * 3 * mat_bytes + x.nbytes + 2 * len(flat) * F * 2 + len(flat) * H * 2
+            if secs > budget_s or layers >= max_layers:
+                break
+    return layers, done, secs
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
+              "see DESIGN.md for how the path would shard", file=sys.stderr)
+        sys.exit(2)
+    from strata_mlx_amd import blocks as B
+    from strata_mlx_amd import synth
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+
+    def note(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    note(f"making {args.layers} IQ3_S layers of 256 experts")
+    lins = decode_layers(B, synth, dev, args.layers)
+    note("decode, batch {}".format(args.tokens))
+    gbs, ms, step_bytes, (gu_bytes, gu_s), routes = decode_bench(B, synth, dev, lins, args.tokens, args.steps,
+                                                                 args.warmup, rng)
+    note(f"decode: {gbs:.1f} GB/s; batch 4")
+    gbs4, ms4, _, (gu4_bytes, gu4_s), _ = decode_bench(B, synth, dev, lins, 4, args.steps, args.warmup, rng)
+    achieved = gu_bytes / gu_s / 1e9
+    result = {
+        "metric": "expert decode matvec GB/s (% HBM peak) + prompt dequant-GEMM TFLOPS",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (random IQ3_S blocks, d=|N(0,1)|*0.01; Zipf(1.1) top-8 routing)",
+        "config": {"workload": f"routed-expert decode, IQ3_S, 256 experts top-8, gate/up 1536x4096, down 4096x1536, "
+                               f"SwiGLU in down, batch {args.tokens}; a step = {args.layers} distinct layers",
+                   "tokens": args.tokens, "experts": E, "top_k": K, "hidden": H, "ffn": F, "layers": args.layers,
+                   "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "decode_t4": {"gbs": round(gbs4, 1), "ms_per_step": round(ms4, 4), "hbm_frac": round(gbs4 / HBM_PEAK_GBS, 4),
+                      "gate_up_kernel_gbs": round(gu4_bytes / gu4_s / 1e9, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "matvec_kernel IQ3_S gate+up (strata_expert_matvec2)",
+                     "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
+    }
+    if not args.no_prompt:
+        note("prompt chunk")
+        result["prompt"] = prompt_bench(B, synth, dev, max(2, args.steps // 10), 2, rng)
+    if not args.no_cpu_baseline:
+        note("cpu baseline")
+        layers, done, secs = cpu_baseline(lins, routes, args.tokens)
+        result["cpu_baseline"] = {"value": round(done / secs / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                                  "sample": f"{layers} layers at batch {args.tokens}: numpy decode of the touched "
+                                            f"experts + float32 matvecs + SwiGLU (oracle/blocks.py), one thread",
+                                  "seconds": round(secs, 2)}
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

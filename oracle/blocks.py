@@ -255,7 +255,12 @@ def expert_matvec(w: np.ndarray, idx: np.ndarray, x: np.ndarray, share: int) -> 
     """out[p] = W[idx[p]] . x[p // share] in float64; w (E, rows, cols). strata_mlx/blocks.py:196-220, 538-554."""
     idx = np.asarray(idx).reshape(-1)
     xs = np.asarray(x, dtype=np.float64).reshape(-1, w.shape[-1])
-    return np.einsum("poi,pi->po", w[idx].astype(np.float64), xs[np.arange(len(idx)) // share])
+    rows = xs[np.arange(len(idx)) // share]
+    out = np.empty((len(idx), w.shape[1]))
+    for e in np.unique(idx):  # an expert at a time: memory of one expert's weights, whatever the pair count
+        at = np.nonzero(idx == e)[0]
+        out[at] = rows[at] @ w[e].astype(np.float64).T
+    return out
 
 
 def swiglu_rounded(g: np.ndarray, u: np.ndarray, dtype) -> np.ndarray:

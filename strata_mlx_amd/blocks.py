@@ -210,5 +210,62 @@ def tileable(kind: str, rows: int, cols: int) -> bool:
     return rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % per_block == 0 and kind not in NO_GRID
 
 
-def _tiled_glu(x, indices, up, gate, down):
-    raise NotImplementedError  # filled in by the tiles section below
+def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
+    """The pairs of `indices` (..., k) laid out in tiles of TOKENS_TILE, each tile one expert's, worked out on the
+    GPU with no host wait: (the expert of each tile, or `experts` for a tile nothing fills; the token of each slot;
+    the slot of each pair), int32, in P // 16 + min(E, P) tiles whatever the routing. An expert's slots go in
+    pair order. strata_mlx/blocks.py:657-681."""
+    k = indices.shape[-1] if indices.ndim else 1
+    flat = _idx32(indices)
+    pairs = flat.numel()
+    lib = _lib.library()
+    n_tiles = lib.strata_route_tiles_max(pairs, experts, TOKENS_TILE)
+    dev = indices.device
+    tile_expert = torch.empty(n_tiles, dtype=torch.int32, device=dev)
+    token = torch.empty(n_tiles * TOKENS_TILE, dtype=torch.int32, device=dev)
+    where = torch.empty(pairs, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(1, lib.strata_route_tiles_workspace(pairs, experts)), dtype=torch.uint8, device=dev)
+    _lib.check(lib.strata_route_tiles(flat.data_ptr(), pairs, k, experts, TOKENS_TILE, tile_expert.data_ptr(),
+                                      token.data_ptr(), where.data_ptr(), None, ws.data_ptr(), _lib.stream()),
+               "tiles_of")
+    return tile_expert, token, where
+
+
+def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, tile_expert: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[p] = W[expert of p's tile] . a[p] for a stack `blocks` of `shape` (experts, rows, cols), on MFMA.
+
+    a (P, cols), P a multiple of TOKENS_TILE, every TOKENS_TILE rows for one expert; tile_expert (P / 16,) says
+    which, or names no expert (>= experts) for a tile to leave out: its rows of the result are then whatever was
+    in memory (in `out` if given). float16/bfloat16 activations multiply weights rounded to float16, float32 ones
+    exact weights; sums are float32. Returns (P, rows) float32. strata_mlx/blocks.py:634-654."""
+    experts, rows, cols = shape
+    _flat_u8(blocks)
+    a = a.contiguous()
+    p = a.shape[0]
+    if p % TOKENS_TILE:
+        raise ValueError(f"{p} rows of activations are not whole tiles of {TOKENS_TILE}")
+    te = tile_expert.reshape(-1).to(torch.int32).contiguous()
+    if te.numel() * TOKENS_TILE != p:
+        raise ValueError("one expert to every tile of activations")
+    if out is None:
+        out = torch.empty((p, rows), dtype=torch.float32, device=a.device)
+    _lib.check(_lib.library().strata_grouped_matmul(
+        _lib.kind_id(kind), blocks.data_ptr(), experts, rows, cols, a.data_ptr(), _lib.dtype_id(a.dtype),
+        te.data_ptr(), te.numel(), TOKENS_TILE, out.data_ptr(), _lib.stream()), f"tile_matmul {kind}")
+    return out
+
+
+def _tiled_glu(x: torch.Tensor, indices: torch.Tensor, up, gate, down) -> torch.Tensor:
+    """The three products of a prompt's pairs through `tile_matmul`, the pairs in tiles (`tiles_of`); the SwiGLU
+    of the float32 products rounded to the activations' type, as strata_mlx/blocks.py:684-694."""
+    tiles, token, where = tiles_of(indices, gate.num_experts)
+    a = x.reshape(-1, x.shape[-1])[token.long()]
+
+    def product(lin, act):
+        return tile_matmul(lin.blocks, lin.kind, (lin.num_experts, lin.output_dims, lin.input_dims), act, tiles)
+
+    g, u = product(gate, a), product(up, a)
+    h = (torch.nn.functional.silu(g) * u).to(x.dtype)
+    out = product(down, h)[where.long()].to(x.dtype)
+    return out.reshape(*indices.shape, down.output_dims)

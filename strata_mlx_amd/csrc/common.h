@@ -54,8 +54,20 @@ template <typename T>
 __device__ __forceinline__ T from_f32(float v);
 template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+// float32 -> float16, round to nearest even, fp16 subnormals included. Left to itself the compiler fuses
+// the conversion into mixed-precision multiplies (v_fma_mix*, v_cvt_pk_f16_f32) that flush subnormal
+// results to zero; the barrier keeps the float32 value as computed, and the subnormal range (|v| < 2^-14)
+// is rounded here: v * 2^24 is exact and below 1024, and rint rounds it to nearest even.
 template <>
-__device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }  // round to nearest even
+__device__ __forceinline__ f16 from_f32<f16>(float v) {
+  asm volatile("" : "+v"(v));
+  const uint32_t u = __float_as_uint(v), a = u & 0x7fffffffu;
+  if (a < 0x38800000u) {
+    const uint32_t m = (uint32_t)__builtin_rintf(__uint_as_float(a) * 16777216.0f);
+    return __builtin_bit_cast(f16, (uint16_t)(((u >> 16) & 0x8000u) | m));
+  }
+  return (f16)v;
+}
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
   uint32_t u = __float_as_uint(v);

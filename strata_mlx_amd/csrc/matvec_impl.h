@@ -91,7 +91,7 @@ __device__ __forceinline__ float swiglu_rounded(XT g, XT u) {
 }
 
 template <int KIND, typename XT, typename OT, bool GLU, int TT>
-__global__ __launch_bounds__(kThreads) void matvec_kernel(MatvecParams p) {
+__global__ __launch_bounds__(kThreads, 2) void matvec_kernel(MatvecParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   StrataTables& tab = *reinterpret_cast<StrataTables*>(smem);
   uint32_t* queue = reinterpret_cast<uint32_t*>(smem + sizeof(StrataTables));
@@ -173,12 +173,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MatvecParams p) {
     if (nq == 0) break;
     done_tokens += nq;
 
-    float acc[TT][kRowsPerLane];
-#pragma unroll
-    for (int t = 0; t < TT; ++t)
-#pragma unroll
-      for (int i = 0; i < kRowsPerLane; ++i) acc[t][i] = 0.0f;
-
+    const int stride = p.ct + 1;
     if (active) {
       float xr[TT][32];
 #pragma unroll
@@ -197,39 +192,25 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MatvecParams p) {
         }
       }
       const int pitch = p.row_ids == nullptr ? p.row_bytes : ((p.row_bytes + 31) & ~15);
+#pragma unroll 1
+      for (int r = lane_row; r < nr; r += p.rs) {  // partial sums straight to LDS: no accumulator array
+        const uint8_t* row = stage + lead + r * pitch;
+        if (p.row_ids != nullptr) {
+          const uint32_t id = p.row_ids[r0 + r];
+          row += (uintptr_t)(mat + (int64_t)(id < (uint32_t)p.src_rows ? id : 0) * p.row_bytes) & 15;
+        }
+        float w[32];
+        strata_unpack32<KIND>(row, c, w, tab);
 #pragma unroll
-      for (int i = 0; i < kRowsPerLane; ++i) {
-        const int r = lane_row + i * p.rs;
-        if (r < nr) {
-          const uint8_t* row = stage + lead + r * pitch;
-          if (p.row_ids != nullptr) {
-            const uint32_t id = p.row_ids[r0 + r];
-            row += (uintptr_t)(mat + (int64_t)(id < (uint32_t)p.src_rows ? id : 0) * p.row_bytes) & 15;
-          }
-          float w[32];
-          strata_unpack32<KIND>(row, c, w, tab);
+        for (int t = 0; t < TT; ++t) {
+          if (t < nq) {
+            float s = 0.0f;
 #pragma unroll
-          for (int t = 0; t < TT; ++t) {
-            if (t < nq) {
-              float s = 0.0f;
-#pragma unroll
-              for (int j = 0; j < 32; ++j) s = __builtin_fmaf(w[j], xr[t][j], s);
-              acc[t][i] = s;
-            }
+            for (int j = 0; j < 32; ++j) s = __builtin_fmaf(w[j], xr[t][j], s);
+            red[(t * p.rt + r) * stride + c] = s;
           }
         }
       }
-    }
-    // partial sums to LDS: red[(t * rt + r) * (ct + 1) + c]
-    const int stride = p.ct + 1;
-    if (active) {
-#pragma unroll
-      for (int t = 0; t < TT; ++t)
-#pragma unroll
-        for (int i = 0; i < kRowsPerLane; ++i) {
-          const int r = lane_row + i * p.rs;
-          if (t < nq && r < nr) red[(t * p.rt + r) * stride + c] = acc[t][i];
-        }
     }
     __syncthreads();
     const int outputs = nq * nr;

@@ -1,6 +1,6 @@
 // One block type's instances of the matvec and dequant kernels. The build compiles this file once per
 // type, with -DSTRATA_KIND=<GGUF type id>, so the types compile in parallel.
-#include "matvec_impl.h"
+#include "fast_impl.h"
 
 #ifndef STRATA_KIND
 #error "STRATA_KIND must name a GGUF type id"
@@ -13,7 +13,7 @@ namespace strata_mv {
 
 int STRATA_CAT(matvec_launch_, STRATA_KIND)(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int grid_y,
                                             int grid_z, hipStream_t s) {
-  return launch_matvec_kind<STRATA_KIND>(p, x_dtype, out_dtype, glu, grid_y, grid_z, s);
+  return launch_matvec_any<STRATA_KIND>(p, x_dtype, out_dtype, glu, grid_y, grid_z, s);
 }
 
 int STRATA_CAT(dequant_launch_, STRATA_KIND)(const uint8_t* blocks, int64_t runs_total, int runs_per_row,
