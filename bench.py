@@ -2,17 +2,17 @@
 """Benchmark of the expert dequant-matmul path on one MI355X.
 
 Headline (value): routed-expert decode matvec, IQ3_S, 256 experts top-8 of Zipf(1.1) routing, gate/up 1536 x 4096
-and down 4096 x 1536 with the SwiGLU in down, float16 activations, batch 1. A step is one decode pass of the
+and down 4096 x 1536, the SwiGLU in gate/up's launch, float16 activations, batch 1. A step is one decode pass of the
 batch through 16 distinct routed-expert layers (about 1 GB of expert bytes, four times the 256 MB MALL), captured
-once as a HIP graph and replayed; each layer is two launches (gate+up, then down with SwiGLU).
+once as a HIP graph and replayed; each layer is two launches (gate+up writing silu(gate) * up, then down).
 value = algorithmic bytes / time: the distinct experts' packed bytes plus activations in and out.
 
 Beside it, on the same line:
   decode_t4   the same at 4 tokens (the other batch of the decode workload)
   prompt      512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, three MFMA
               grouped products; TFLOPS over the real pairs' 2 * pairs * 3 * 4096 * 1536 flops
-  roofline    the dominant kernel (gate+up matvec): algorithmic bytes per launch / its mean duration (HIP
-              events around a graph of those launches only), against 8 TB/s
+  roofline    the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
+              (HIP events around a graph of those launches only), against 8 TB/s
   cpu_baseline the oracle's numpy decode + matvec (the reference's CPU path restated) on a few layers
 """
 
@@ -79,24 +79,24 @@ def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):  # one eager pass first: the library's lazy state, torch's allocator
         for (gate, up, down), ix in zip(lins, idx):
-            g_, u_ = B.gate_up(gate, up, x, ix, K)
-            B.matvec_glu(down, ix.reshape(-1), g_, u_)
+            h = B.gate_up_swiglu(gate, up, x, ix, K)[2]
+            B.expert_matvec(down, ix.reshape(-1), h)
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     full, gu = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(full):
         for (gate, up, down), ix in zip(lins, idx):
-            g_, u_ = B.gate_up(gate, up, x, ix, K)
-            B.matvec_glu(down, ix.reshape(-1), g_, u_)
+            h = B.gate_up_swiglu(gate, up, x, ix, K)[2]
+            B.expert_matvec(down, ix.reshape(-1), h)
     with torch.cuda.graph(gu):
         for (gate, up, down), ix in zip(lins, idx):
-            B.gate_up(gate, up, x, ix, K)
+            B.gate_up_swiglu(gate, up, x, ix, K)
     step_bytes, gu_bytes = 0, 0
     for r in routes:
         d = len(np.unique(r))
-        act = tokens * H * 2 + 2 * tokens * K * F * 2  # x in; g, u out
+        act = tokens * H * 2 + tokens * K * F * 2  # x in; silu(gate) * up out (gate and up themselves not counted)
         gu_bytes += d * 2 * mat_bytes + act
-        step_bytes += d * 3 * mat_bytes + act + 2 * tokens * K * F * 2 + tokens * K * H * 2  # g, u in; y out
+        step_bytes += d * 3 * mat_bytes + act + tokens * K * F * 2 + tokens * K * H * 2  # down: h in, y out
     t = time_graph(full, steps, warmup)
     t_gu = time_graph(gu, steps, warmup)
     launches = steps * len(lins)
@@ -191,14 +191,14 @@ def main():
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic (random IQ3_S blocks, d=|N(0,1)|*0.01; Zipf(1.1) top-8 routing)",
         "config": {"workload": f"routed-expert decode, IQ3_S, 256 experts top-8, gate/up 1536x4096, down 4096x1536, "
-                               f"SwiGLU in down, batch {args.tokens}; a step = {args.layers} distinct layers",
+                               f"SwiGLU in gate/up, batch {args.tokens}; a step = {args.layers} distinct layers",
                    "tokens": args.tokens, "experts": E, "top_k": K, "hidden": H, "ffn": F, "layers": args.layers,
                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
         "decode_t4": {"gbs": round(gbs4, 1), "ms_per_step": round(ms4, 4), "hbm_frac": round(gbs4 / HBM_PEAK_GBS, 4),
                       "gate_up_kernel_gbs": round(gu4_bytes / gu4_s / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "matvec_kernel IQ3_S gate+up (strata_expert_matvec2)",
+                     "kernel": "direct_decode_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
                      "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
     }
     if not args.no_prompt:

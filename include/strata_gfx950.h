@@ -62,6 +62,16 @@ int strata_expert_matvec2(int kind, const void* blocks_a, const void* blocks_b, 
                           int64_t cols, const uint32_t* idx, int64_t pairs, const void* x, int x_dtype,
                           int64_t share, void* out_a, void* out_b, void* stream);
 
+/* strata_expert_matvec2 over the gate and up stacks that also writes out_h = swiglu(out_gate, out_up)
+ * rounded as strata_expert_matvec_swiglu rounds it; out_gate, out_up, out_h (pairs, rows). The float16
+ * IQ3_S / IQ3_XXS / Q2_0 kernels do it in the one launch (a lane holds both sums of a row); others add a
+ * small elementwise launch. Replaces the gate and up calls of switch_glu and the swiglu of its down call,
+ * strata_mlx/blocks.py:969-975 with _MATVEC_GLU's rounding, strata_mlx/blocks.py:222-236. */
+int strata_expert_gate_up_swiglu(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts,
+                                 int64_t rows, int64_t cols, const uint32_t* idx, int64_t pairs, const void* x,
+                                 int x_dtype, int64_t share, void* out_gate, void* out_up, void* out_h,
+                                 void* stream);
+
 /* out[p, r] = W[idx[p], r, :] . swiglu(gate[p], up[p]) with the SwiGLU rounded as mlx-lm rounds it
  * (sigmoid in float32 rounded to the activation dtype, then two products in that dtype); gate, up
  * (pairs, cols). Replaces matvec_glu + _MATVEC_GLU, strata_mlx/blocks.py:939-955, 225-259. */

@@ -119,6 +119,38 @@ def gate_up(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tensor, idx
     return g, u
 
 
+def gate_up_swiglu(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tensor, idx: torch.Tensor, share: int):
+    """gate_up with silu(gate) * up as well, rounded as mlx-lm rounds it: three (pairs, out). IQ3_S, IQ3_XXS and
+    Q2_0 in float16 do it in one launch (a lane ends with both sums of a row); other types and dtypes add a small
+    elementwise launch. The gate and up calls of strata_mlx/blocks.py:969-975 with the SwiGLU of its down call."""
+    if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) != (up.kind, up.output_dims, up.input_dims,
+                                                                             up.num_experts):
+        raise ValueError("gate and up differ in type or shape")
+    pairs = idx.numel()
+    x2 = x.reshape(-1, gate.input_dims).contiguous()
+    g = torch.empty((pairs, gate.output_dims), dtype=x.dtype, device=x.device)
+    u, h = torch.empty_like(g), torch.empty_like(g)
+    idx = _idx32(idx)
+    _lib.check(_lib.library().strata_expert_gate_up_swiglu(
+        _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), gate.num_experts, gate.output_dims,
+        gate.input_dims, idx.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), share, g.data_ptr(),
+        u.data_ptr(), h.data_ptr(), _lib.stream()), f"gate/up/swiglu {gate.kind}")
+    return g, u, h
+
+
+def expert_matvec(lin: BlockSwitchLinear, idx: torch.Tensor, x: torch.Tensor, share: int = 1) -> torch.Tensor:
+    """out[pair] = W[idx[pair]] . x[pair / share]: x (pairs / share, in) -> (pairs, out)."""
+    pairs = idx.numel()
+    x2 = x.reshape(-1, lin.input_dims).contiguous()
+    out = torch.empty((pairs, lin.output_dims), dtype=x.dtype, device=x.device)
+    idx = _idx32(idx)
+    _lib.check(_lib.library().strata_expert_matvec(
+        _lib.kind_id(lin.kind), lin.blocks.data_ptr(), lin.num_experts, lin.output_dims, lin.input_dims,
+        idx.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), share, out.data_ptr(), _lib.stream()),
+        f"matvec {lin.kind}")
+    return out
+
+
 def matvec_glu(lin: BlockSwitchLinear, idx: torch.Tensor, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """`lin(swiglu(gate, up), idx)`, one pair to each row of gate and up: (pairs, out). The SwiGLU is rounded as
     mlx-lm rounds it. strata_mlx/blocks.py:939-955."""
@@ -172,8 +204,8 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, ga
     """down(silu(gate(x)) * up(x)) through each token's experts: x (..., in), indices (..., k) -> (..., k, out).
     The argument order is the reference's (x, indices, up, gate, down); strata_mlx/blocks.py:958-986.
 
-    Decode windows take the matvec kernels: gate and up in one launch reading x once, then down with the SwiGLU
-    worked out in its own registers, rounded as mlx-lm rounds it. Prompt chunks (from TILES_FROM pairs) take the
+    Decode windows take the matvec kernels: gate and up in one launch reading x once and writing silu(gate) * up
+    (rounded as mlx-lm rounds it), then down on that. Prompt chunks (from TILES_FROM pairs) take the
     tiles: the pairs sorted by expert on the GPU, weights decoded into LDS and multiplied on MFMA."""
     indices = torch.as_tensor(indices, device=x.device)
     k = indices.shape[-1] if indices.ndim else 1
@@ -182,8 +214,10 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, ga
     if flat.numel() >= TILES_FROM and all(tileable(lin.kind, lin.output_dims, lin.input_dims)
                                           for lin in (up, gate, down)):
         return _tiled_glu(x, indices, up, gate, down)
-    if (gate.kind, gate.output_dims, gate.input_dims) == (up.kind, up.output_dims, up.input_dims):
-        g, u = gate_up(gate, up, xs, flat, k)
+    if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) == (up.kind, up.output_dims, up.input_dims,
+                                                                             up.num_experts):
+        _, _, h = gate_up_swiglu(gate, up, xs, flat, k)
+        return expert_matvec(down, flat, h).reshape(*indices.shape, down.output_dims)
     else:
         g = gate(xs.reshape(-1, 1, 1, xs.shape[-1]).expand(-1, 1, 1, -1), indices.reshape(-1, k)).reshape(flat.numel(), -1)
         u = up(xs.reshape(-1, 1, 1, xs.shape[-1]).expand(-1, 1, 1, -1), indices.reshape(-1, k)).reshape(flat.numel(), -1)

@@ -1,0 +1,464 @@
+// The decode matvec for float16 activations, rows read straight into registers (IQ3_S, IQ3_XXS, Q2_0).
+//
+// A decode call moves tens of megabytes in a few microseconds, so what matters is that every byte is requested
+// at once: a wave's loads go out as soon as it knows its expert, before anything else it does. Nothing is staged
+// in LDS except the codebooks. A lane takes two consecutive runs of one block (64 weights) of a row and loads
+// exactly their fields into registers (IQ3_S: the 16 index bytes, the two high-bit bytes, the eight sign bytes,
+// the scale byte and d: five loads at 2-byte alignment, which gfx950 serves as they are). A row is L lanes (its
+// run pairs rounded up to a power of two: 64 for 4096 inputs, 32 for 1536), 64 / L rows side by side; a wave
+// takes RU such row steps of one matrix (a "unit"), all loaded before the first is decoded. Codebook entries
+// come from LDS as float16 and sign masks (as in fast_impl.h), products from v_dot2_f32_f16 against the
+// activations packed in registers, and a row's partial sums meet across its lanes by shuffles.
+//
+// The routed form gives a wave (pair, stack, rows). A pair whose expert an earlier pair names leaves its rows to
+// that pair's waves, which multiply them by every pair naming the expert (ballots over the pairs' ids, TT pairs
+// a pass). When every pair multiplies the same token (one token's gate/up), the rows are multiplied once and the
+// sum is written for every pair naming the expert.
+//
+// Paired mode (gate and up of one call): a unit's row steps alternate between the two stacks, the same rows of
+// each, so the lane that ends with row r's gate sum also has its up sum, and writes silu(gate) * up as mlx-lm
+// rounds it (strata_mlx/blocks.py:222-236): the down projection then reads one float16 vector a pair.
+#pragma once
+#include "decode_impl.h"
+
+namespace strata_mv {
+
+constexpr int kDMaxPairs = 256;  // pairs the direct kernel takes (four ballots)
+
+// the fields of two consecutive runs of a block, as one lane holds them
+template <int KIND>
+struct RunPair;
+template <>
+struct RunPair<K_IQ3_S> {
+  u32x4 qs;     // 16 index bytes
+  uint32_t qh;  // two high-bit bytes
+  u32x2 sg;     // eight sign bytes
+  uint32_t sc;  // the scale byte: low nibble the first run's, high the second's
+  uint32_t d;
+};
+template <>
+struct RunPair<K_IQ3_XXS> {
+  u32x4 qs;
+  u32x2 aux;    // the two runs' scale and sign words
+  uint32_t d;
+};
+template <>
+struct RunPair<K_Q2_0> {
+  u32x4 qs;     // the block's 16 code bytes
+  uint32_t d;
+};
+
+// A load from global memory at any alignment (gfx950 serves 2-byte aligned dwordx2/x4 loads as they are).
+template <typename T>
+struct __attribute__((packed, aligned(1))) Unaligned {
+  T v;
+};
+template <typename T>
+__device__ __forceinline__ T load_unaligned(const uint8_t* p) {
+  typedef const __attribute__((address_space(1))) Unaligned<T> GlobalT;
+  return ((GlobalT*)(const __attribute__((address_space(1))) uint8_t*)p)->v;
+}
+
+__device__ __forceinline__ float half_bits(uint32_t b) { return (float)__builtin_bit_cast(f16, (uint16_t)b); }
+
+// run pair j of a row (runs 2j, 2j + 1)
+template <int KIND>
+__device__ __forceinline__ void load_pair(const uint8_t* row, int j, RunPair<KIND>& f) {
+  if constexpr (KIND == K_IQ3_S) {  // d @0, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106
+    const uint8_t* b = row + (j >> 2) * 110;
+    const int ib0 = 2 * (j & 3);
+    f.d = load_unaligned<uint16_t>(b);
+    f.qs = load_unaligned<u32x4>(b + 2 + 8 * ib0);
+    f.qh = load_unaligned<uint16_t>(b + 66 + ib0);
+    f.sg = load_unaligned<u32x2>(b + 74 + 4 * ib0);
+    f.sc = load_unaligned<uint8_t>(b + 106 + (j & 3));
+  } else if constexpr (KIND == K_IQ3_XXS) {  // d @0, qs[64] @2, aux[8] (u32) @66
+    const uint8_t* b = row + (j >> 2) * 98;
+    const int ib0 = 2 * (j & 3);
+    f.d = load_unaligned<uint16_t>(b);
+    f.qs = load_unaligned<u32x4>(b + 2 + 8 * ib0);
+    f.aux = load_unaligned<u32x2>(b + 66 + 4 * ib0);
+  } else {  // Q2_0: d @0, qs[16] @2
+    const uint8_t* b = row + j * 18;
+    f.d = load_unaligned<uint16_t>(b);
+    f.qs = load_unaligned<u32x4>(b + 2);
+  }
+}
+
+// run h (0, 1) of a pair: 16 packed float16 pairs of integers, and the run's scale
+template <int KIND>
+__device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint32_t* w, const FastTables<KIND>& t) {
+  const float d = half_bits(f.d);
+  if constexpr (KIND == K_IQ3_S) {  // strata_mlx/blocks.py:89-102
+    const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
+    const uint32_t qh = (f.qh >> (8 * h)) & 255, sg = f.sg[h];
+    const float scale = d * (float)(1 + 2 * ((f.sc >> (4 * h)) & 15));
+    // the ninth index bits of four groups spread into bytes, then interleaved with the qs bytes by v_perm
+    const uint32_t hb0 = (__builtin_amdgcn_ubfe(qh, 0, 4) * 0x204081u) & 0x01010101u;
+    const uint32_t hb1 = (__builtin_amdgcn_ubfe(qh, 4, 4) * 0x204081u) & 0x01010101u;
+    const uint32_t i01 = __builtin_amdgcn_perm(hb0, qs0, 0x05010400u), i23 = __builtin_amdgcn_perm(hb0, qs0, 0x07030602u);
+    const uint32_t i45 = __builtin_amdgcn_perm(hb1, qs1, 0x05010400u), i67 = __builtin_amdgcn_perm(hb1, qs1, 0x07030602u);
+    const uint32_t ix[8] = {i01 & 0xffff, i01 >> 16, i23 & 0xffff, i23 >> 16,
+                            i45 & 0xffff, i45 >> 16, i67 & 0xffff, i67 >> 16};
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const u32x2 g = t.grid[ix[l]];
+      const u32x4 m = t.signs[(sg >> (8 * (l >> 1))) & 255];
+      w[2 * l] = g[0] ^ m[(l & 1) * 2];
+      w[2 * l + 1] = g[1] ^ m[(l & 1) * 2 + 1];
+    }
+    return scale;
+  } else if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116
+    const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
+    const uint32_t aux = f.aux[h];
+    const float scale = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const u32x2 g = t.grid[((l < 4 ? qs0 : qs1) >> (8 * (l & 3))) & 255];
+      const u32x4 m = t.signs[(aux >> (7 * (l >> 1))) & 127];
+      w[2 * l] = g[0] ^ m[(l & 1) * 2];
+      w[2 * l + 1] = g[1] ^ m[(l & 1) * 2 + 1];
+    }
+    return scale;
+  } else {  // Q2_0, strata_mlx/blocks.py:58-68
+    const uint32_t q0 = f.qs[2 * h], q1 = f.qs[2 * h + 1];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x2 c = t.q2[((i < 4 ? q0 : q1) >> (8 * (i & 3))) & 255];
+      w[2 * i] = c[0];
+      w[2 * i + 1] = c[1];
+    }
+    return d;
+  }
+}
+
+// The codebook tables in two halves: the constants' loads go out before the rows' (a wait for them is then not
+// a wait for the rows), the LDS entries are written after.
+template <int KIND>
+struct TableFetch {
+  uint32_t g[2] = {0, 0};
+};
+template <int KIND>
+__device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
+  if constexpr (FastTraits<KIND>::grid > 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = min(tid + k * kThreads, FastTraits<KIND>::grid - 1);
+      tf.g[k] = KIND == K_IQ3_S ? kStrataIq3sGrid[i] : kStrataIq3xxsGrid[i];
+    }
+  }
+}
+template <int KIND>
+__device__ __forceinline__ void store_tables(FastTables<KIND>& t, const TableFetch<KIND>& tf, int tid) {
+  if constexpr (FastTraits<KIND>::grid > 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = tid + k * kThreads;
+      const uint32_t g = tf.g[k];
+      if (i < FastTraits<KIND>::grid)
+        t.grid[i] = u32x2{pack_h2((float)(g & 255), (float)((g >> 8) & 255)),
+                          pack_h2((float)((g >> 16) & 255), (float)(g >> 24))};
+    }
+  }
+  if constexpr (FastTraits<KIND>::signs > 0) {
+    for (int i = tid; i < FastTraits<KIND>::signs; i += kThreads)
+      t.signs[i] = sign_masks(KIND == K_IQ3_XXS ? strata_ksign((uint32_t)i) : (uint32_t)i);
+  }
+  if constexpr (FastTraits<KIND>::q2 > 0) {
+    for (int i = tid; i < 256; i += kThreads)
+      t.q2[i] = u32x2{pack_h2((float)(i & 3) - 1.0f, (float)((i >> 2) & 3) - 1.0f),
+                      pack_h2((float)((i >> 4) & 3) - 1.0f, (float)(i >> 6) - 1.0f)};
+  }
+}
+
+// The compiler no longer knows the fields' values: code that decodes them cannot move above this point.
+template <int KIND>
+__device__ __forceinline__ void opaque(RunPair<KIND>& f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(f.qs[i]));
+  asm volatile("" : "+v"(f.d));
+  if constexpr (KIND == K_IQ3_S) {
+    asm volatile("" : "+v"(f.qh), "+v"(f.sc), "+v"(f.sg[0]), "+v"(f.sg[1]));
+  } else if constexpr (KIND == K_IQ3_XXS) {
+    asm volatile("" : "+v"(f.aux[0]), "+v"(f.aux[1]));
+  }
+}
+
+// the lowest pair left in the four masks, taken out; -1 when none is
+__device__ __forceinline__ int take_lowest(uint64_t& m) {
+  const int b = __ffsll((unsigned long long)m) - 1;
+  m &= m - 1;
+  return b;
+}
+__device__ __forceinline__ int take_member(uint64_t& m0, uint64_t& m1, uint64_t& m2, uint64_t& m3) {
+  if (m0) return take_lowest(m0);
+  if (m1) return 64 + take_lowest(m1);
+  if (m2) return 128 + take_lowest(m2);
+  if (m3) return 192 + take_lowest(m3);
+  return -1;
+}
+
+// Unit geometry: p.ct lanes to a row, p.rt rows of each matrix a unit, p.ntiles units to a matrix, p.nz stacks
+// taken as separate units (1 in paired mode), p.items units in all. Every load before the first wait has no
+// branch around it: rows past the end and lanes past a row's run pairs load the last row / run pair again, and
+// an expert id out of range loads expert 0's rows and writes NaN.
+template <int KIND, bool GLU, bool PAIRED, int TT, int RU>
+__global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)) void direct_decode_kernel(MatvecParams p) {
+  __shared__ FastTables<KIND> tab;
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int L = p.ct;
+  const int side = 64 / L;  // rows side by side
+  const int sub = lane / L, ln = lane % L;
+  const int npr = p.runs / 2;
+  const bool live = ln < npr;
+  const int jp = min(ln, npr - 1);
+  constexpr int kSteps = PAIRED ? RU / 2 : RU;  // row steps of each matrix
+
+  const int unit = blockIdx.x * kWaves + wave;
+  const bool in_range = unit < p.items;
+  const int u = in_range ? unit : 0;
+  const int per_pair = p.nz * p.ntiles;
+  const int pair = u / per_pair, rem = u % per_pair;
+  const int z0 = rem / p.ntiles;
+  const int r0 = (rem % p.ntiles) * p.rt;
+
+  const uint8_t* m0;
+  const uint8_t* m1 = nullptr;
+  uint32_t expert = 0;
+  bool bad = false;
+  if (p.mode == MODE_EXPERT) {
+    expert = p.idx[pair];
+    bad = expert >= (uint64_t)p.experts;
+    const int64_t off = (int64_t)(bad ? 0u : expert) * p.mat_bytes;
+    m0 = p.blocks[PAIRED ? 0 : z0] + off;
+    if (PAIRED) m1 = p.blocks[1] + off;
+  } else if (p.mode == MODE_PTRS) {
+    m0 = p.ptrs[pair];
+  } else {
+    m0 = p.blocks[z0];
+  }
+
+  // loads in the order they are waited for: the tables' constants and the pairs' ids, the activations, the rows
+  TableFetch<KIND> tf;
+  fetch_tables<KIND>(tf, tid);
+  uint32_t e[4] = {0, 0, 0, 0};
+  if (p.mode == MODE_EXPERT) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
+  }
+  const bool one_x = p.mode == MODE_EXPERT && !GLU && p.share == p.pairs;  // every pair the same token
+  uint32_t x[TT][32];
+  const int q0 = p.mode == MODE_DENSE ? 0 : pair;
+  if constexpr (!GLU) {
+    fast_load_x<false>(p, q0, 2 * jp, x[0]);
+    fast_load_x<false>(p, q0, 2 * jp + 1, x[0] + 16);
+  }
+  RunPair<KIND> f[RU];
+#pragma unroll
+  for (int s = 0; s < RU; ++s) {
+    const int r = min(r0 + (PAIRED ? s / 2 : s) * side + sub, p.rows - 1);
+    load_pair<KIND>((PAIRED && (s & 1) ? m1 : m0) + (int64_t)r * p.row_bytes, jp, f[s]);
+  }
+  if constexpr (GLU) {  // silu(gate) * up waits for its loads: after the rows' have gone out
+    fast_load_x<true>(p, q0, 2 * jp, x[0]);
+    fast_load_x<true>(p, q0, 2 * jp + 1, x[0] + 16);
+  }
+  // nothing above moves below this point, nothing below moves above it
+  asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(tf.g[0]), "+v"(tf.g[1])::"memory");
+  // the pairs naming this expert from this one on; a wave whose expert an earlier pair names has no work
+  uint64_t mb0 = 0, mb1 = 0, mb2 = 0, mb3 = 0;
+  bool valid = in_range;
+  store_tables<KIND>(tab, tf, tid);
+  if (p.mode == MODE_EXPERT && !bad) {
+    bool earlier = false;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint64_t m = __ballot(64 * c + lane < p.pairs && e[c] == expert);
+      const int lo = pair - 64 * c;  // bits below lo are earlier pairs
+      const uint64_t below = lo <= 0 ? 0ull : (lo >= 64 ? ~0ull : ((1ull << lo) - 1));
+      earlier |= (m & below) != 0;
+      const uint64_t mine = m & ~below;
+      if (c == 0) mb0 = mine;
+      if (c == 1) mb1 = mine;
+      if (c == 2) mb2 = mine;
+      if (c == 3) mb3 = mine;
+    }
+    valid = valid && !earlier;
+  }
+  __syncthreads();
+  if (!valid) return;
+  if (bad) {  // a pair naming no expert: NaN
+    const f16 nan = (f16)__builtin_nanf("");
+    for (int r = r0 + lane; r < min(r0 + p.rt, p.rows); r += 64) {
+      const int64_t o = (int64_t)pair * p.rows + r;
+      if (p.out[PAIRED ? 0 : z0] != nullptr) reinterpret_cast<f16*>(p.out[PAIRED ? 0 : z0])[o] = nan;
+      if (PAIRED && p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = nan;
+      if (PAIRED) reinterpret_cast<f16*>(p.glu_out)[o] = nan;
+    }
+    return;
+  }
+
+  int done = 0;  // window: tokens done
+  for (int pass = 0;; ++pass) {
+    int q[TT];
+    int nq = 0;
+    if (p.mode == MODE_DENSE) {
+      nq = max(0, min(TT, p.tokens - done));
+#pragma unroll
+      for (int t = 0; t < TT; ++t) q[t] = done + t;
+      done += nq;
+    } else if (p.mode == MODE_PTRS || one_x) {
+      nq = pass == 0 ? 1 : 0;
+#pragma unroll
+      for (int t = 0; t < TT; ++t) q[t] = pair;
+    } else {
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        q[t] = take_member(mb0, mb1, mb2, mb3);
+        nq += q[t] >= 0;
+      }
+    }
+    if (nq == 0) break;
+#pragma unroll
+    for (int st = 0; st < RU; ++st) opaque(f[st]);  // decoded anew each pass, not hoisted out of the loop
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t < nq && (pass > 0 || t > 0)) {
+        fast_load_x<GLU>(p, q[t], 2 * jp, x[t]);
+        fast_load_x<GLU>(p, q[t], 2 * jp + 1, x[t] + 16);
+      }
+    }
+    float sums[RU][TT];
+#pragma unroll
+    for (int s = 0; s < RU; ++s) {
+      const int r = r0 + (PAIRED ? s / 2 : s) * side + sub;
+      float acc[TT];
+#pragma unroll
+      for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t w[16];
+        const float scale = decode_pair<KIND>(f[s], h, w, tab);
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+          if (t < nq) acc[t] += scale * dot16x2(w, x[t] + 16 * h);
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        float v = live && r < p.rows ? acc[t] : 0.0f;
+        for (int o = L / 2; o >= 1; o /= 2) v += __shfl_xor(v, o, L);
+        sums[s][t] = v;
+      }
+    }
+    // lane 0 of each row writes: the pass's pairs, or (one token) every pair naming the expert
+    if (ln == 0) {
+#pragma unroll
+      for (int k = 0; k < kSteps; ++k) {
+        const int r = r0 + k * side + sub;
+        if (r >= p.rows) continue;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          if (t >= nq) continue;
+          uint64_t a0 = mb0, a1 = mb1, a2 = mb2, a3 = mb3;
+          for (int qq = one_x ? pair : q[t]; qq >= 0; qq = one_x ? take_member(a0, a1, a2, a3) : -1) {
+            if (one_x && qq == pair) take_member(a0, a1, a2, a3);  // the pair itself is the lowest member
+            const int64_t o = (int64_t)qq * p.rows + r;
+            if constexpr (PAIRED) {
+              const f16 g = from_f32<f16>(sums[2 * k][t]), uu = from_f32<f16>(sums[2 * k + 1][t]);
+              if (p.out[0] != nullptr) reinterpret_cast<f16*>(p.out[0])[o] = g;
+              if (p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = uu;
+              reinterpret_cast<f16*>(p.glu_out)[o] = from_f32<f16>(swiglu_rounded<f16>(g, uu));
+            } else {
+              reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(sums[k][t]);
+            }
+          }
+        }
+      }
+    }
+    if (one_x || p.mode == MODE_PTRS) break;
+  }
+}
+
+// Row steps a unit takes: 4, or STRATA_ROW_STEPS (2, 4, 6 or 8) to tune it.
+inline int row_steps() {
+  static const int v = [] {
+    const char* e = getenv("STRATA_ROW_STEPS");
+    const int r = e ? atoi(e) : 4;
+    return (r == 2 || r == 4 || r == 6 || r == 8) ? r : 4;
+  }();
+  return v;
+}
+
+template <int KIND, bool GLU, bool PAIRED, int TT, int RU>
+int launch_direct_ru(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
+  const int side = 64 / p.ct;
+  p.tt = TT;
+  p.nz = PAIRED ? 1 : grid_z;
+  p.rt = (PAIRED ? RU / 2 : RU) * side;
+  p.ntiles = (p.rows + p.rt - 1) / p.rt;
+  const int64_t units = (int64_t)grid_y * p.nz * p.ntiles;
+  if (units > INT32_MAX - kWaves) return STRATA_ERR_SHAPE;
+  p.items = (int)units;
+  const int grid = (int)((units + kWaves - 1) / kWaves);
+  hipLaunchKernelGGL((direct_decode_kernel<KIND, GLU, PAIRED, TT, RU>), dim3(grid), dim3(kThreads), 0, stream, p);
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
+template <int KIND, bool GLU, bool PAIRED, int TT>
+int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
+  switch (row_steps()) {
+    case 2: return launch_direct_ru<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
+    case 6: return launch_direct_ru<KIND, GLU, PAIRED, TT, 6>(p, grid_y, grid_z, s);
+    case 8: return launch_direct_ru<KIND, GLU, PAIRED, TT, 8>(p, grid_y, grid_z, s);
+    default: return launch_direct_ru<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
+  }
+}
+
+// Rows of 64 to 4096 weights in run pairs (every IQ3_S / IQ3_XXS / Q2_0 row), up to 256 pairs.
+inline bool direct_takes(const MatvecParams& p) {
+  const int runs = p.cols / 32;
+  return runs % 2 == 0 && runs >= 2 && runs / 2 <= 64 && (p.mode != MODE_EXPERT || p.pairs <= kDMaxPairs);
+}
+
+template <int KIND, bool GLU, bool PAIRED>
+int launch_direct(MatvecParams& p, bool one_token, int grid_y, int grid_z, hipStream_t s) {
+  p.runs = p.cols / 32;
+  int L = 1;
+  while (L < p.runs / 2) L *= 2;
+  p.ct = L;
+  if (one_token) return launch_direct_tt<KIND, GLU, PAIRED, 1>(p, grid_y, grid_z, s);
+  return launch_direct_tt<KIND, GLU, PAIRED, 2>(p, grid_y, grid_z, s);
+}
+
+// The float16 fast paths where they apply (a type of FastTraits, float16 in and out, rows contiguous): the
+// direct kernel, else the persistent wave kernel, else the staged fast kernel; other cases the generic kernels.
+template <int KIND>
+int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int grid_y, int grid_z, hipStream_t s) {
+  if constexpr (FastTraits<KIND>::supported) {
+    if (x_dtype == DT_F16 && out_dtype == DT_F16 && p.row_ids == nullptr) {
+      const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
+                                                                     : (glu ? p.pairs <= 16 : p.pairs <= p.share));
+      if (p.glu_out != nullptr) {
+        if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
+        return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
+      }
+      if (direct_takes(p)) {
+        return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
+                   : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);
+      }
+      int rpl = 0;
+      if ((p.mode == MODE_DENSE || p.pairs <= kPMaxPairs) && wave_lanes(p.cols / 32, &rpl) > 0) {
+        return glu ? launch_wave_rpl<KIND, true>(p, one, grid_y, grid_z, s)
+                   : launch_wave_rpl<KIND, false>(p, one, grid_y, grid_z, s);
+      }
+      if (glu) return one ? launch_fast<KIND, true, 1>(p, grid_y, grid_z, s) : launch_fast<KIND, true, 4>(p, grid_y, grid_z, s);
+      return one ? launch_fast<KIND, false, 1>(p, grid_y, grid_z, s) : launch_fast<KIND, false, 4>(p, grid_y, grid_z, s);
+    }
+  }
+  if (p.glu_out != nullptr) return STRATA_ERR_SHAPE;
+  return launch_matvec_kind<KIND>(p, x_dtype, out_dtype, glu, grid_y, grid_z, s);
+}
+
+}  // namespace strata_mv

@@ -359,17 +359,4 @@ int launch_fast(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
 
 // The float16 fast path where it applies (a type of FastTraits, float16 in and out, rows contiguous), else the
 // generic kernels. One token's pairs (or a window of one token) hold one token a pass, others four.
-template <int KIND>
-int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int grid_y, int grid_z, hipStream_t s) {
-  if constexpr (FastTraits<KIND>::supported) {
-    if (x_dtype == DT_F16 && out_dtype == DT_F16 && p.row_ids == nullptr) {
-      const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
-                                                                     : (glu ? p.pairs <= 16 : p.pairs <= p.share));
-      if (glu) return one ? launch_fast<KIND, true, 1>(p, grid_y, grid_z, s) : launch_fast<KIND, true, 4>(p, grid_y, grid_z, s);
-      return one ? launch_fast<KIND, false, 1>(p, grid_y, grid_z, s) : launch_fast<KIND, false, 4>(p, grid_y, grid_z, s);
-    }
-  }
-  return launch_matvec_kind<KIND>(p, x_dtype, out_dtype, glu, grid_y, grid_z, s);
-}
-
 }  // namespace strata_mv

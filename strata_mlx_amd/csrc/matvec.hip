@@ -76,16 +76,38 @@ int block_shape(int kind, int64_t rows, int64_t cols, int* row_bytes) {
 
 bool valid_dtype(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
 
+template <typename XT>
+__global__ void swiglu_kernel(const XT* g, const XT* u, XT* h, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) h[i] = from_f32<XT>(swiglu_rounded<XT>(g[i], u[i]));
+}
+
+// h = silu(g) * u over n elements, rounded as mlx-lm rounds it
+int launch_swiglu(const void* g, const void* u, void* h, int64_t n, int dtype, hipStream_t s) {
+  const int64_t blocks = (n + 255) / 256;
+  if (blocks > INT32_MAX) return STRATA_ERR_SHAPE;
+  if (dtype == DT_F16)
+    hipLaunchKernelGGL(swiglu_kernel<f16>, dim3((int)blocks), dim3(256), 0, s, (const f16*)g, (const f16*)u, (f16*)h, n);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL(swiglu_kernel<bf16_t>, dim3((int)blocks), dim3(256), 0, s, (const bf16_t*)g, (const bf16_t*)u,
+                       (bf16_t*)h, n);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<float>, dim3((int)blocks), dim3(256), 0, s, (const float*)g, (const float*)u,
+                       (float*)h, n);
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
 int expert_common(int kind, const void* a, const void* b, int64_t experts, int64_t rows, int64_t cols,
                   const uint32_t* idx, int64_t pairs, const void* x, const void* up, int dtype, int64_t share,
-                  void* out_a, void* out_b, bool glu, void* stream) {
+                  void* out_a, void* out_b, bool glu, void* stream, void* out_h = nullptr) {
   MatvecParams p = {};
   int rc = block_shape(kind, rows, cols, &p.row_bytes);
   if (rc) return rc;
   if (!valid_dtype(dtype)) return STRATA_ERR_DTYPE;
   if (pairs < 0 || experts < 0 || experts > INT32_MAX) return STRATA_ERR_ARG;
   if (pairs == 0 || rows == 0) return STRATA_OK;
-  if (!a || !idx || !x || !out_a || (b && !out_b) || (glu && !up)) return STRATA_ERR_ARG;
+  if (experts == 0 || !a || !idx || !x || !out_a || (b && !out_b) || (glu && !up)) return STRATA_ERR_ARG;
   if (share < 1 || pairs % share) return STRATA_ERR_ARG;
   if (pairs > 65535 || cols / 32 > 256) return STRATA_ERR_SHAPE;
   p.blocks[0] = (const uint8_t*)a;
@@ -103,6 +125,15 @@ int expert_common(int kind, const void* a, const void* b, int64_t experts, int64
   p.pairs = (int)pairs;
   p.share = (int)share;
   p.mode = MODE_EXPERT;
+  if (out_h != nullptr) {  // gate and up with silu(gate) * up: one launch where the float16 kernels take it
+    p.glu_out = out_h;
+    rc = launch_by_kind(kind, p, dtype, dtype, false, (int)pairs, 2, (hipStream_t)stream);
+    if (rc != STRATA_ERR_SHAPE) return rc;
+    p.glu_out = nullptr;
+    rc = launch_by_kind(kind, p, dtype, dtype, false, (int)pairs, 2, (hipStream_t)stream);
+    if (rc) return rc;
+    return launch_swiglu(out_a, out_b, out_h, pairs * rows, dtype, (hipStream_t)stream);
+  }
   return launch_by_kind(kind, p, dtype, dtype, glu, (int)pairs, b ? 2 : 1, (hipStream_t)stream);
 }
 
@@ -144,6 +175,14 @@ int strata_expert_matvec2(int kind, const void* blocks_a, const void* blocks_b, 
   if (!blocks_b && pairs > 0 && rows > 0) return STRATA_ERR_ARG;
   return expert_common(kind, blocks_a, blocks_b, experts, rows, cols, idx, pairs, x, nullptr, x_dtype, share, out_a,
                        out_b, false, stream);
+}
+
+int strata_expert_gate_up_swiglu(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts,
+                                 int64_t rows, int64_t cols, const uint32_t* idx, int64_t pairs, const void* x,
+                                 int x_dtype, int64_t share, void* out_gate, void* out_up, void* out_h, void* stream) {
+  if ((!up_blocks || !out_h) && pairs > 0 && rows > 0) return STRATA_ERR_ARG;
+  return expert_common(kind, gate_blocks, up_blocks, experts, rows, cols, idx, pairs, x, nullptr, x_dtype, share,
+                       out_gate, out_up, false, stream, out_h);
 }
 
 int strata_expert_matvec_swiglu(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,

@@ -33,6 +33,7 @@ struct MatvecParams {
   const uint32_t* row_ids;     // dense mode: rows to compute, or null for all
   const void* x;               // activations, or gate in GLU mode
   const void* up;              // GLU mode
+  void* glu_out;               // paired gate/up mode: silu(gate) * up, rounded as mlx-lm rounds it
   int64_t mat_bytes;           // rows_in_matrix * row_bytes
   int64_t experts;             // expert mode: matrices in the stack
   int src_rows;                // rows of the matrix (row_ids must be below it)
@@ -41,6 +42,7 @@ struct MatvecParams {
   int pairs, share, tokens;
   int ct, rs, rt;              // column threads (= runs), row lanes, rows per tile
   int tt;                      // tokens a pass holds in registers (<= TT)
+  int nz, ntiles, items;       // persistent decode: stacks, row tiles per matrix, work items
   int mode;
   int stage_bytes;             // LDS bytes for the staged rows
 };

@@ -1,6 +1,6 @@
 // One block type's instances of the matvec and dequant kernels. The build compiles this file once per
 // type, with -DSTRATA_KIND=<GGUF type id>, so the types compile in parallel.
-#include "fast_impl.h"
+#include "direct_impl.h"
 
 #ifndef STRATA_KIND
 #error "STRATA_KIND must name a GGUF type id"

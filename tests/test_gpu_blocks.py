@@ -207,3 +207,73 @@ def test_listed_rows_have_the_layers_own_bits(gpu):
     assert torch.equal(got, full[:, ids.long()])
     bad = B.window_matvec(blocks, "Q6_K", 400, 256, x, row_ids=torch.tensor([1, 400], dtype=torch.int32, device=gpu))
     assert torch.isfinite(bad[0, 0]) and torch.isnan(bad[0, 1])
+
+
+def _h_matches_swiglu(h, g, u):
+    """h against the oracle's SwiGLU of the same g, u: equal, or one float16 step apart where the device expf and
+    the oracle's exp round a sigmoid differently (at most 1 in 100 elements)."""
+    want = O.swiglu_rounded(g, u, np.float16)
+    hb, wb = h.view(np.int16).astype(np.int32), want.view(np.int16).astype(np.int32)
+    off = hb != wb
+    assert np.abs(hb - wb).max() <= 1
+    assert off.mean() <= 0.01
+
+
+@pytest.mark.parametrize("kind,dtype", [("IQ3_S", torch.float16), ("IQ3_XXS", torch.float16), ("Q2_0", torch.float16),
+                                        ("Q4_K", torch.float16), ("IQ3_S", torch.float32)])
+def test_gate_up_with_swiglu_gives_gate_up_and_their_swiglu(gpu, kind, dtype):
+    """The paired launch (float16 IQ3_S / IQ3_XXS / Q2_0) and the two-launch form (other types and dtypes) give
+    gate_up's own bits for gate and up, and the SwiGLU of those bits."""
+    rng = np.random.default_rng(11)
+    per = O.BY_NAME[kind][1]
+    E, F, H, tokens, k = 8, 96, 1024, 3, 4
+    stacks = [O.random_blocks(kind, E * F * H // per, rng, scale="normal") for _ in range(2)]
+    gate, up = (B.BlockSwitchLinear(dev(d, gpu), kind, (E, F, H)) for d in stacks)
+    idx = dev(np.stack([rng.choice(E, k, replace=False) for _ in range(tokens)]).reshape(-1), gpu)
+    x = dev((rng.standard_normal((tokens, H)) / 16).astype(np.float32), gpu).to(dtype)
+    g0, u0 = B.gate_up(gate, up, x, idx, k)
+    g, u, h = B.gate_up_swiglu(gate, up, x, idx, k)
+    assert torch.equal(g, g0) and torch.equal(u, u0)
+    if dtype == torch.float16:
+        _h_matches_swiglu(h.cpu().numpy(), g.cpu().numpy(), u.cpu().numpy())
+    else:
+        want = O.swiglu_rounded(g.cpu().numpy(), u.cpu().numpy(), np.float32)
+        np.testing.assert_allclose(h.cpu().numpy(), want, rtol=1e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "IQ3_XXS", "Q2_0"])
+@pytest.mark.parametrize("rows,cols", [(37, 512), (64, 2048), (5, 4096)])
+def test_many_pairs_on_few_experts_match_each_pair_alone(gpu, kind, rows, cols):
+    """200 pairs (25 tokens x top-8) over 16 experts: an expert's rows are read once and multiplied by every pair
+    naming it. Each pair gets the bits it gets alone, and the products are the oracle's within 1e-3 relative L2.
+    Rows that do not fill a work unit (37, 5) and rows shorter than a wave (512, 2048 inputs) included."""
+    rng = np.random.default_rng(rows)
+    per = O.BY_NAME[kind][1]
+    E, tokens, k = 16, 25, 8
+    data = O.random_blocks(kind, E * rows * cols // per, rng, scale="normal")
+    lin = B.BlockSwitchLinear(dev(data, gpu), kind, (E, rows, cols))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(tokens)])
+    x = (rng.standard_normal((tokens, cols)) / 32).astype(np.float16)
+    xs, flat = dev(x, gpu), dev(idx.reshape(-1), gpu)
+    together = B.expert_matvec(lin, flat, xs, k)
+    per_token = B.expert_matvec(lin, flat, torch.repeat_interleave(xs, k, 0), 1)
+    assert torch.equal(together, per_token)
+    for p in (0, 7, 64, 130, 199):
+        alone = B.expert_matvec(lin, flat[p:p + 1], xs[p // k:p // k + 1], 1)
+        assert torch.equal(alone[0], together[p])
+    w = O.dequantize(data, kind, (E, rows, cols))
+    want = O.expert_matvec(w, idx.reshape(-1), x, k)
+    got = together.float().cpu().numpy()
+    assert np.linalg.norm(got - want) <= 1e-3 * np.linalg.norm(want)
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "IQ3_XXS", "Q2_0"])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 5, 12])
+def test_a_float16_window_on_codebook_types(gpu, kind, tokens):
+    data, w = tensor(kind, tokens, rows=40, cols=1024)
+    x = (torch.randn((tokens, 1024), generator=torch.Generator().manual_seed(tokens)) / 8).half()
+    got = B.window_matvec(dev(data, gpu), kind, 40, 1024, x.to(gpu)).float().cpu().numpy()
+    want = x.double().numpy() @ w.astype(np.float64).T
+    assert np.abs(got - want).max() <= 4e-3 * np.abs(want).max()
+    one = B.window_matvec(dev(data, gpu), kind, 40, 1024, x[:1].to(gpu)).float().cpu().numpy()
+    assert np.array_equal(one[0], got[0])
