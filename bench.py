@@ -42,7 +42,25 @@ def parse():
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prompt", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also copy 512 MiB with torch's copy kernel three times: the known-size reference that "
+                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "direct_decode_gate_up_iq3s_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per gate+up launch as rocprofv3's counters gave them (the committed summary), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(line.split("=")[1].strip())
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def time_graph(graph, steps, warmup):
@@ -177,6 +195,13 @@ def main():
     def note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
+    if args.copy_probe:
+        src = torch.ones(512 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     note(f"making {args.layers} IQ3_S layers of 256 experts")
     lins = decode_layers(B, synth, dev, args.layers)
     note("decode, batch {}".format(args.tokens))
@@ -197,7 +222,7 @@ def main():
         "decode_t4": {"gbs": round(gbs4, 1), "ms_per_step": round(ms4, 4), "hbm_frac": round(gbs4 / HBM_PEAK_GBS, 4),
                       "gate_up_kernel_gbs": round(gu4_bytes / gu4_s / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "direct_decode_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
                      "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
     }

@@ -6,9 +6,9 @@
  * the file lays it out: row r of matrix e starts at byte (e * rows + r) * row_bytes, where
  * row_bytes = cols / weights_per_block * bytes_per_block.
  *
- * Every pointer except `row_ids` of strata_dense_matvec is a device pointer, and every call only
- * enqueues work on `stream` (a hipStream_t; NULL is the default stream). The library allocates
- * nothing and never waits for the device. The caller owns all memory: inputs are only read and
+ * Every pointer is a device pointer (so is each of strata_expert_matvec_ptrs's per_pair), and every
+ * call only enqueues work on `stream` (a hipStream_t; NULL is the default stream). The library
+ * allocates nothing and never waits for the device. The caller owns all memory: inputs are only read and
  * outputs are fully written. Calls are reentrant across host threads and streams.
  * Activation/output dtypes: STRATA_F32, STRATA_F16, STRATA_BF16. Sums are float32 throughout.
  *
@@ -50,8 +50,8 @@ int strata_dequant(int kind, const void* blocks, int64_t n_mats, int64_t rows, i
 
 /* out[p, r] = W[idx[p], r, :] . x[p / share, :] for p < pairs, W a stack of `experts` matrices of
  * rows x cols; out (pairs, rows) in x's dtype. Pairs that name the same expert read its bytes once.
- * idx values must be < experts. Replaces BlockSwitchLinear.__call__ + _MATVEC,
- * strata_mlx/blocks.py:538-554, 196-220. */
+ * A pair naming no expert (idx >= experts) gets NaN rows; experts must be at least 1 when pairs > 0.
+ * Replaces BlockSwitchLinear.__call__ + _MATVEC, strata_mlx/blocks.py:538-554, 196-220. */
 int strata_expert_matvec(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
                          const uint32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share,
                          void* out, void* stream);

@@ -10,6 +10,19 @@ Every weight is an exact float32 value (an fp16 scale times small integers), so 
 float64 and rounding once to float32 is exactly the reference's float32 result. Q4_K and Q5_K are the
 exception: `code * (d * sc) + -(dmin * mn)`, one rounding at the add; those are computed in float32
 in the reference's order (strata_mlx/gguf.py:207-217, test_gguf.py:55).
+
+What pins each function (tests/test_oracle.py; the reference holds no golden vectors for this path):
+  - every decoder: a second, scalar C restatement (unpack.c) agrees bit for bit; closed forms for Q2_0
+    (test_gguf.py:34-38 of the reference), Q8_0, Q4_0, Q5_0; encoders restated from ggml's quantize packing
+    round-trip through Q4_K, Q6_K, Q3_K; IQ3_S, IQ3_XXS, IQ4_XS moved one field at a time.
+  - IQ3_S / IQ3_XXS codebook values: parity unpinned against the reference's own tables (gguf-py 0.19.0, which
+    builds them at run time, is absent here). Two transcriptions in different encodings agree entry by entry and
+    have ggml's structure; no vector from the reference confirms them.
+  - expert_matvec / tile_matmul: float64 products of the decoded weights (the reference's test oracles,
+    test_blocks.py:35, 107); the summation order of the reference's Q4_K / Q8_0 products (mlx) is not restated.
+  - tiles_of: the invariants of test_blocks.py:177-195.
+  - swiglu_rounded: the rounding steps of strata_mlx/blocks.py:222-238, checked against float64 silu within the
+    half-ulp bounds those steps allow.
 """
 
 import numpy as np

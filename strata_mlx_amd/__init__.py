@@ -5,9 +5,10 @@ kernels behind a C ABI (include/strata_gfx950.h, libstrata_gfx950.so). The Pytho
 reference's call surface with torch tensors on the GPU:
 
     blocks   BlockSwitchLinear, BlockSwitchGLU, dequantize, window_matvec, matvec_glu, matvec_separate,
-             tiles_of, tile_matmul, switch_glu            (strata_mlx/blocks.py)
-    dense    ScaledLinear, BlockLinear, BlockEmbedding    (strata_mlx/dense.py)
-    rows     GuessRows row layers on listed lm_head rows (strata_mlx/rows.py)
+             gate_up_swiglu, tiles_of, tile_matmul, switch_glu          (strata_mlx/blocks.py)
+    dense    ScaledLinear, BlockLinear, BlockEmbedding                  (strata_mlx/dense.py)
+    rows     rows_of, GuessRows: listed rows of an output layer         (strata_mlx/rows.py)
+    synth    synthetic blocks and Zipf routing for benchmarks and tests
 """
 
-__all__ = ["blocks"]
+__all__ = ["blocks", "dense", "rows", "synth"]

@@ -1,0 +1,115 @@
+"""Dense layers on the file's blocks: the call surface of strata_mlx/dense.py, over `strata_dense_matvec`.
+
+    ScaledLinear   a Q6_K layer given as the reference holds it (codes, scales, d; dense.py:109-167). The parts
+                   are packed back into the file's Q6_K blocks once, on the GPU, and every product reads those
+                   210-byte blocks (6.56 bits a weight, where the parts take 8.56).
+    BlockLinear    a layer kept as the file's blocks, any type the kernels decode (dense.py:205-242); `inputs`
+                   reorders the activations as the reference's does.
+    BlockEmbedding rows of an embedding decoded when their tokens come (dense.py:245-258).
+
+Up to MAX_TOKENS tokens a product is a window of the matvec kernel (each block decoded once for every token); a
+longer chunk multiplies the dequantized weights as floats (torch's GEMM), as the reference does.
+"""
+
+import torch
+
+from . import blocks as B
+
+MAX_TOKENS = 8  # more than a window: a chunk of a prompt, multiplied as floats (dense.py:33)
+
+
+def q6k_blocks(codes: torch.Tensor, scales: torch.Tensor, d: torch.Tensor) -> torch.Tensor:
+    """The Q6_K blocks (rows * cols / 256 * 210 bytes, uint8) whose parts are `codes` int8 (rows, cols) in
+    [-32, 31], `scales` int8 (rows, cols / 16) and `d` float16 (rows, cols / 256): the inverse of q6k_parts
+    (strata_mlx/gguf.py:150-165). In a block, weight 128h + 32r + i has its low four bits in ql[64h + i] (r = 0,
+    2: low / high nibble) or ql[64h + 32 + i] (r = 1, 3), its high two in bits 2r of qh[32h + i]."""
+    rows, cols = codes.shape
+    if cols % 256 or scales.shape != (rows, cols // 16) or d.shape != (rows, cols // 256):
+        raise ValueError(f"Q6_K parts of a ({rows}, {cols}) layer must be codes (rows, cols), scales "
+                         f"(rows, cols/16), d (rows, cols/256)")
+    nb = cols // 256
+    q = (codes.to(torch.int16) + 32).to(torch.uint8).reshape(rows, nb, 2, 4, 32)
+    lo, hi = q & 15, q >> 4
+    ql = torch.cat([lo[:, :, :, 0] | (lo[:, :, :, 2] << 4), lo[:, :, :, 1] | (lo[:, :, :, 3] << 4)], dim=3)
+    qh = hi[:, :, :, 0] | (hi[:, :, :, 1] << 2) | (hi[:, :, :, 2] << 4) | (hi[:, :, :, 3] << 6)
+    sc = scales.contiguous().view(torch.uint8).reshape(rows, nb, 16)
+    dd = d.to(torch.float16).contiguous().view(torch.uint8).reshape(rows, nb, 2)
+    return torch.cat([ql.reshape(rows, nb, 128), qh.reshape(rows, nb, 64), sc, dd], dim=2).reshape(-1)
+
+
+class BlockLinear:
+    """A linear layer held as the file's blocks; called like `nn.Linear`. strata_mlx/dense.py:205-242.
+
+    `blocks` are the rows in the order of the layer's outputs. `inputs`, if given, is where in the file's row
+    each input is: the activations are reordered to the file's order before they multiply."""
+
+    def __init__(self, blocks: torch.Tensor, kind: str, shape: tuple, inputs=None):
+        self.blocks, self.kind = B._flat_u8(blocks), kind
+        self.output_dims, self.input_dims = shape
+        if blocks.numel() < self.output_dims * B.row_bytes(kind, self.input_dims):
+            raise ValueError("blocks hold fewer bytes than the shape needs")
+        self.to_file = None
+        if inputs is not None:
+            self.to_file = torch.argsort(torch.as_tensor(inputs, device=blocks.device)).to(torch.int64)
+
+    @property
+    def nbytes(self) -> int:
+        return self.blocks.numel()
+
+    def floats(self, dtype: torch.dtype) -> torch.Tensor:
+        """The weights (out, in), each exact in float32 and rounded once to `dtype`."""
+        w = B.dequantize(self.blocks, self.kind, (self.output_dims, self.input_dims),
+                         torch.float16 if dtype == torch.float16 else torch.float32)
+        return w if w.dtype == dtype else w.to(dtype)
+
+    def __call__(self, x: torch.Tensor, row_ids: torch.Tensor | None = None) -> torch.Tensor:
+        rows, cols = self.output_dims, self.input_dims
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, cols)
+        if self.to_file is not None:
+            x2 = x2[:, self.to_file]
+        tokens = x2.shape[0]
+        if tokens <= MAX_TOKENS or row_ids is not None:
+            out = B.window_matvec(self.blocks, self.kind, rows, cols, x2, row_ids=row_ids)
+        else:
+            out = x2 @ self.floats(x.dtype).T
+        return out.reshape(*lead, out.shape[-1])
+
+
+class ScaledLinear(BlockLinear):
+    """A Q6_K layer given as codes, scales and d (strata_mlx/dense.py:109-167), kept as the file's Q6_K blocks.
+    d_step (weights to a d) must be 256: layers whose inputs were reordered are BlockLinear with `inputs`."""
+
+    def __init__(self, codes: torch.Tensor, scales: torch.Tensor, d: torch.Tensor):
+        rows, cols = codes.shape
+        if d.shape[1] * 256 != cols:
+            raise ValueError(f"a d to every {cols // max(1, d.shape[1])} weights: only 256 (the file's blocks)")
+        super().__init__(q6k_blocks(codes, scales, d), "Q6_K", (rows, cols))
+
+    @classmethod
+    def from_blocks(cls, blocks: torch.Tensor, shape: tuple) -> "ScaledLinear":
+        """A layer straight from the file's Q6_K bytes."""
+        self = cls.__new__(cls)
+        BlockLinear.__init__(self, blocks, "Q6_K", shape)
+        return self
+
+
+class BlockEmbedding:
+    """An embedding held as the file's blocks; a token's row is decoded when the token comes.
+    strata_mlx/dense.py:245-258."""
+
+    def __init__(self, blocks: torch.Tensor, kind: str, shape: tuple, dtype: torch.dtype):
+        self.num_embeddings, self.dims = shape
+        self.kind, self.dtype = kind, dtype
+        self.rows = B._flat_u8(blocks).reshape(self.num_embeddings, -1)
+
+    @property
+    def nbytes(self) -> int:
+        return self.rows.numel()
+
+    def __call__(self, ids: torch.Tensor) -> torch.Tensor:
+        ids = torch.as_tensor(ids, device=self.rows.device)
+        taken = self.rows.index_select(0, ids.reshape(-1).to(torch.int64)).reshape(-1)
+        dt = torch.float16 if self.dtype == torch.float16 else torch.float32
+        out = B.dequantize(taken, self.kind, (ids.numel(), 1, self.dims), dt)
+        return out.to(self.dtype).reshape(*ids.shape, self.dims)

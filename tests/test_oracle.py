@@ -11,8 +11,10 @@
 - Field-by-field checks of IQ3_S / IQ3_XXS / IQ4_XS: one field changed at a time moves exactly the weights it
   should, by exactly the factor it should.
 - tiles_of's invariants (tests/test_blocks.py:177-195 of the reference).
+- The committed vectors of tests/golden/ (the oracle's own output at a fixed seed) are reproduced bit for bit.
 """
 
+import os
 import re
 
 import numpy as np
@@ -327,3 +329,29 @@ def test_swiglu_rounding_is_within_half_ulps_of_silu():
     gf, uf = g.astype(np.float64), u.astype(np.float64)
     exact = gf / (1 + np.exp(-gf)) * uf
     assert np.abs(got - exact).max() <= 4 * 2 ** -11 * np.abs(exact).max()
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "oracle_vectors.npz")
+
+
+def test_the_oracle_still_gives_the_committed_vectors():
+    """tests/golden/oracle_vectors.npz (written by tests/golden/make_golden.py): every decoder, the routed matvec,
+    the tile layout and the SwiGLU give the committed numbers, bit for bit."""
+    gold = np.load(GOLDEN)
+    kinds = sorted({k.split("/")[0] for k in gold.files if k.endswith("/blocks") and "/" in k} - {"matvec"})
+    assert len(kinds) == 11
+    for kind in kinds:
+        data = gold[f"{kind}/blocks"]
+        per = O.BY_NAME[kind][1]
+        n = data.size // O.BY_NAME[kind][2]
+        assert np.array_equal(O.dequantize(data, kind, (1, n * per)).astype(np.float32), gold[f"{kind}/weights"])
+    w = O.dequantize(gold["matvec/blocks"], "IQ3_S", (3, 2, 256))
+    assert np.array_equal(O.expert_matvec(w, gold["matvec/idx"], gold["matvec/x"], 2), gold["matvec/out"])
+    te, token, where = O.tiles_of(gold["tiles/indices"], 5, 16)
+    assert np.array_equal(te, gold["tiles/tile_expert"]) and np.array_equal(token, gold["tiles/token"])
+    assert np.array_equal(where, gold["tiles/where"])
+    g, u = gold["swiglu/g"], gold["swiglu/u"]
+    assert np.array_equal(O.swiglu_rounded(g, u, np.float16), gold["swiglu/h16"])
+    assert np.array_equal(O.swiglu_rounded(g.astype(np.float32), u.astype(np.float32), np.float32),
+                          gold["swiglu/h32"])
+
