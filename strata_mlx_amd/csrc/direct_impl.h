@@ -24,6 +24,7 @@
 namespace strata_mv {
 
 constexpr int kDMaxPairs = 256;  // pairs the direct kernel takes (four ballots)
+constexpr int kDMaxCols = 4096;  // inputs of a row the direct kernel takes (64 lanes of 64)
 
 // the fields of two consecutive runs of a block, as one lane holds them
 template <int KIND>
@@ -198,16 +199,98 @@ __device__ __forceinline__ int take_member(uint64_t& m0, uint64_t& m1, uint64_t&
   return -1;
 }
 
-// Unit geometry: p.ct lanes to a row, p.rt rows of each matrix a unit, p.ntiles units to a matrix, p.nz stacks
-// taken as separate units (1 in paired mode), p.items units in all. Every load before the first wait has no
-// branch around it: rows past the end and lanes past a row's run pairs load the last row / run pair again, and
-// an expert id out of range loads expert 0's rows and writes NaN.
-template <int KIND, bool GLU, bool PAIRED, int TT, int RU>
-__global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)) void direct_decode_kernel(MatvecParams p) {
+// Per-lane byte offsets of a lane's run pair j within a row (the same for every row of a unit).
+template <int KIND>
+struct LaneOffsets {
+  uint32_t d, qs, a, b, c;  // IQ3_S: d, qs, qh (a), signs (b), scale (c); IQ3_XXS: d, qs, aux (a); Q2_0: d, qs
+};
+template <int KIND>
+__device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
+  LaneOffsets<KIND> o{};
+  if constexpr (KIND == K_IQ3_S) {  // d @0, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106
+    const uint32_t b = (j >> 2) * 110, jj = j & 3;
+    o.d = b;
+    o.qs = b + 2 + 16 * jj;
+    o.a = b + 66 + 2 * jj;
+    o.b = b + 74 + 8 * jj;
+    o.c = b + 106 + jj;
+  } else if constexpr (KIND == K_IQ3_XXS) {  // d @0, qs[64] @2, aux[8] (u32) @66
+    const uint32_t b = (j >> 2) * 98, jj = j & 3;
+    o.d = b;
+    o.qs = b + 2 + 16 * jj;
+    o.a = b + 66 + 8 * jj;
+  } else {  // Q2_0: d @0, qs[16] @2
+    o.d = j * 18;
+    o.qs = j * 18 + 2;
+  }
+  return o;
+}
+
+// A load at base + off: base the same for the whole wave, off the lane's (global_load v, v_off, s_base).
+template <typename T>
+__device__ __forceinline__ T load_at(const uint8_t* base, uint32_t off) {
+  typedef const __attribute__((address_space(1))) Unaligned<T> GlobalT;
+  const __attribute__((address_space(1))) uint8_t* b = (const __attribute__((address_space(1))) uint8_t*)base;
+  return ((GlobalT*)(b + off))->v;
+}
+
+template <int KIND>
+__device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, const LaneOffsets<KIND>& o,
+                                            RunPair<KIND>& f) {
+  f.d = load_at<uint16_t>(row, lo + o.d);
+  f.qs = load_at<u32x4>(row, lo + o.qs);
+  if constexpr (KIND == K_IQ3_S) {
+    f.qh = load_at<uint16_t>(row, lo + o.a);
+    f.sg = load_at<u32x2>(row, lo + o.b);
+    f.sc = load_at<uint8_t>(row, lo + o.c);
+  } else if constexpr (KIND == K_IQ3_XXS) {
+    f.aux = load_at<u32x2>(row, lo + o.a);
+  }
+}
+
+// v from the lane whose index differs in bit d (d = 1, 2, 4, 8: DPP within rows of 16; 16, 32: permute). For
+// d = 4 and 8 the partner is the mirror lane within 8 / 16 lanes, which also differs in bit d: a reduction or an
+// exchange between the two halves needs only that.
+__device__ __forceinline__ float lanes_apart(float v, int d) {
+  const int b = __float_as_int(v);
+  if (d == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false));   // quad_perm 1032
+  if (d == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false));   // quad_perm 2301
+  if (d == 4) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  if (d == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x140, 0xF, 0xF, false));  // row_mirror
+  return __shfl_xor(v, d);
+}
+
+// N partial sums a lane (N row steps) over rows of L lanes -> the lanes of group ln / (L / N) hold the total of
+// row step ln / (L / N). Exchange halves first (N - 1 moves), then reduce the one value left (log2(L / N)).
+template <int L, int N>
+__device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
+#pragma unroll
+  for (int n = N, d = L / 2; n > 1; n /= 2, d /= 2) {
+    const bool up = (ln & d) != 0;
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i) {
+      const float send = up ? v[i] : v[i + n / 2];
+      const float keep = up ? v[i + n / 2] : v[i];
+      v[i] = keep + lanes_apart(send, d);
+    }
+  }
+  float s = v[0];
+#pragma unroll
+  for (int d = L / N / 2; d >= 1; d /= 2) s += lanes_apart(s, d);
+  return s;
+}
+
+// Unit geometry: L lanes to a row (LT when known at compile time, else p.ct), p.rt rows of each matrix a unit,
+// p.ntiles units to a matrix, p.nz stacks taken as separate units (1 in paired mode), p.items units in all.
+// Every load before the first wait has no branch around it: rows past the end and lanes past a row's run
+// pairs load the last row / run pair again, and an expert id out of range loads expert 0's rows and writes NaN.
+template <int KIND, bool GLU, bool PAIRED, int TT, int RU, int LT>
+__global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kernel(MatvecParams p) {
   __shared__ FastTables<KIND> tab;
+  __shared__ u32x4 xs[kDMaxCols / 8];  // one token's activations, when every wave multiplies the same token
   const int tid = threadIdx.x, lane = tid % 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-  const int L = p.ct;
+  const int L = LT > 0 ? LT : p.ct;
   const int side = 64 / L;  // rows side by side
   const int sub = lane / L, ln = lane % L;
   const int npr = p.runs / 2;
@@ -248,17 +331,28 @@ __global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)
     for (int c = 0; c < 4; ++c) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
   }
   const bool one_x = p.mode == MODE_EXPERT && !GLU && p.share == p.pairs;  // every pair the same token
+  // one token for the whole workgroup (one token's routed pairs, a window's first token): read once, coalesced,
+  // into LDS; otherwise each lane reads its own 128 bytes
+  const bool shared_x = !GLU && (one_x || p.mode == MODE_DENSE);
   uint32_t x[TT][32];
   const int q0 = p.mode == MODE_DENSE ? 0 : pair;
-  if constexpr (!GLU) {
+  u32x4 xv[2];
+  if (shared_x) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.x);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) xv[k] = src[min(tid + k * kThreads, p.cols / 8 - 1)];
+  } else if constexpr (!GLU) {
     fast_load_x<false>(p, q0, 2 * jp, x[0]);
     fast_load_x<false>(p, q0, 2 * jp + 1, x[0] + 16);
   }
+  const LaneOffsets<KIND> lo = lane_offsets<KIND>(jp);
   RunPair<KIND> f[RU];
 #pragma unroll
   for (int s = 0; s < RU; ++s) {
-    const int r = min(r0 + (PAIRED ? s / 2 : s) * side + sub, p.rows - 1);
-    load_pair<KIND>((PAIRED && (s & 1) ? m1 : m0) + (int64_t)r * p.row_bytes, jp, f[s]);
+    const int rb = r0 + (PAIRED ? s / 2 : s) * side;  // the step's first row, the same for the whole wave
+    const int rw = min(rb, p.rows - 1), rl = min(rb + sub, p.rows - 1);
+    const uint8_t* row = (PAIRED && (s & 1) ? m1 : m0) + (int64_t)rw * p.row_bytes;
+    load_fields<KIND>(row, (uint32_t)(rl - rw) * p.row_bytes, lo, f[s]);
   }
   if constexpr (GLU) {  // silu(gate) * up waits for its loads: after the rows' have gone out
     fast_load_x<true>(p, q0, 2 * jp, x[0]);
@@ -270,13 +364,18 @@ __global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)
   uint64_t mb0 = 0, mb1 = 0, mb2 = 0, mb3 = 0;
   bool valid = in_range;
   store_tables<KIND>(tab, tf, tid);
+  if (shared_x) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (tid + k * kThreads < p.cols / 8) xs[tid + k * kThreads] = xv[k];
+  }
   if (p.mode == MODE_EXPERT && !bad) {
     bool earlier = false;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint64_t m = __ballot(64 * c + lane < p.pairs && e[c] == expert);
-      const int lo = pair - 64 * c;  // bits below lo are earlier pairs
-      const uint64_t below = lo <= 0 ? 0ull : (lo >= 64 ? ~0ull : ((1ull << lo) - 1));
+      const int lo_bits = pair - 64 * c;  // bits below are earlier pairs
+      const uint64_t below = lo_bits <= 0 ? 0ull : (lo_bits >= 64 ? ~0ull : ((1ull << lo_bits) - 1));
       earlier |= (m & below) != 0;
       const uint64_t mine = m & ~below;
       if (c == 0) mb0 = mine;
@@ -288,6 +387,14 @@ __global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)
   }
   __syncthreads();
   if (!valid) return;
+  if (shared_x) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const u32x4 c = xs[8 * jp + v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[0][4 * v + i] = c[i];
+    }
+  }
   if (bad) {  // a pair naming no expert: NaN
     const f16 nan = (f16)__builtin_nanf("");
     for (int r = r0 + lane; r < min(r0 + p.rt, p.rows); r += 64) {
@@ -299,6 +406,9 @@ __global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)
     return;
   }
 
+  // the transposed reduction needs the row length at compile time and no more row steps than lanes to a row
+  constexpr bool kFast = LT > 0 && RU <= LT;
+  constexpr int G = kFast ? LT / RU : 1;  // lanes holding one row step's total after the reduction
   int done = 0;  // window: tokens done
   for (int pass = 0;; ++pass) {
     int q[TT];
@@ -329,68 +439,108 @@ __global__ __launch_bounds__(kThreads, TT * RU <= 4 ? 4 : (TT * RU <= 8 ? 3 : 2)
         fast_load_x<GLU>(p, q[t], 2 * jp + 1, x[t] + 16);
       }
     }
-    float sums[RU][TT];
+    float acc[TT][RU];
+    float sums[RU][TT];  // row sums of the run-time reduction
 #pragma unroll
     for (int s = 0; s < RU; ++s) {
       const int r = r0 + (PAIRED ? s / 2 : s) * side + sub;
-      float acc[TT];
 #pragma unroll
-      for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
+      for (int t = 0; t < TT; ++t) acc[t][s] = 0.0f;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         uint32_t w[16];
         const float scale = decode_pair<KIND>(f[s], h, w, tab);
 #pragma unroll
         for (int t = 0; t < TT; ++t)
-          if (t < nq) acc[t] += scale * dot16x2(w, x[t] + 16 * h);
+          if (t < nq) acc[t][s] += scale * dot16x2(w, x[t] + 16 * h);
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        float v = live && r < p.rows ? acc[t] : 0.0f;
-        for (int o = L / 2; o >= 1; o /= 2) v += __shfl_xor(v, o, L);
-        sums[s][t] = v;
+        acc[t][s] = live && r < p.rows ? acc[t][s] : 0.0f;
+        if constexpr (!kFast) {
+          float v = acc[t][s];
+          for (int o = L / 2; o >= 1; o /= 2) v += __shfl_xor(v, o, L);
+          sums[s][t] = v;
+        }
       }
     }
-    // lane 0 of each row writes: the pass's pairs, or (one token) every pair naming the expert
-    if (ln == 0) {
+    if constexpr (kFast) {
+      // one write sequence for every row of the unit: lane ln of group g = ln / G holds row step g's total
+      const int g = ln / G;
+      const bool writer = ln % (PAIRED ? 2 * G : G) == 0;
+      const int k = PAIRED ? g / 2 : g;  // the row step of its matrix
+      const int r = r0 + k * side + sub;
 #pragma unroll
-      for (int k = 0; k < kSteps; ++k) {
-        const int r = r0 + k * side + sub;
-        if (r >= p.rows) continue;
-#pragma unroll
-        for (int t = 0; t < TT; ++t) {
-          if (t >= nq) continue;
+      for (int t = 0; t < TT; ++t) {
+        if (t >= nq) continue;
+        const float v = reduce_steps<LT, RU>(acc[t], ln);
+        float h = 0.0f;
+        f16 gq, uq;
+        if constexpr (PAIRED) {  // gate in group 2k, up in group 2k + 1
+          const float up = lanes_apart(v, G);
+          gq = from_f32<f16>(v);
+          uq = from_f32<f16>(up);
+          h = swiglu_rounded<f16>(gq, uq);
+        }
+        if (writer && r < p.rows) {
           uint64_t a0 = mb0, a1 = mb1, a2 = mb2, a3 = mb3;
-          for (int qq = one_x ? pair : q[t]; qq >= 0; qq = one_x ? take_member(a0, a1, a2, a3) : -1) {
-            if (one_x && qq == pair) take_member(a0, a1, a2, a3);  // the pair itself is the lowest member
+          for (int qq = one_x ? take_member(a0, a1, a2, a3) : q[t]; qq >= 0;
+               qq = one_x ? take_member(a0, a1, a2, a3) : -1) {
             const int64_t o = (int64_t)qq * p.rows + r;
             if constexpr (PAIRED) {
-              const f16 g = from_f32<f16>(sums[2 * k][t]), uu = from_f32<f16>(sums[2 * k + 1][t]);
-              if (p.out[0] != nullptr) reinterpret_cast<f16*>(p.out[0])[o] = g;
-              if (p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = uu;
-              reinterpret_cast<f16*>(p.glu_out)[o] = from_f32<f16>(swiglu_rounded<f16>(g, uu));
+              if (p.out[0] != nullptr) reinterpret_cast<f16*>(p.out[0])[o] = gq;
+              if (p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = uq;
+              reinterpret_cast<f16*>(p.glu_out)[o] = from_f32<f16>(h);
             } else {
-              reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(sums[k][t]);
+              reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(v);
+            }
+          }
+        }
+      }
+    } else {
+      // lane 0 of each row writes: the pass's pairs, or (one token) every pair naming the expert
+      if (ln == 0) {
+#pragma unroll
+        for (int kk = 0; kk < kSteps; ++kk) {
+          const int r = r0 + kk * side + sub;
+          if (r >= p.rows) continue;
+#pragma unroll
+          for (int t = 0; t < TT; ++t) {
+            if (t >= nq) continue;
+            uint64_t a0 = mb0, a1 = mb1, a2 = mb2, a3 = mb3;
+            for (int qq = one_x ? take_member(a0, a1, a2, a3) : q[t]; qq >= 0;
+                 qq = one_x ? take_member(a0, a1, a2, a3) : -1) {
+              const int64_t o = (int64_t)qq * p.rows + r;
+              if constexpr (PAIRED) {
+                const f16 gg = from_f32<f16>(sums[2 * kk][t]), uu = from_f32<f16>(sums[2 * kk + 1][t]);
+                if (p.out[0] != nullptr) reinterpret_cast<f16*>(p.out[0])[o] = gg;
+                if (p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = uu;
+                reinterpret_cast<f16*>(p.glu_out)[o] = from_f32<f16>(swiglu_rounded<f16>(gg, uu));
+              } else {
+                reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(sums[kk][t]);
+              }
             }
           }
         }
       }
     }
-    if (one_x || p.mode == MODE_PTRS) break;
+    if (p.mode != MODE_EXPERT && (p.mode == MODE_PTRS || (p.mode == MODE_DENSE && done >= p.tokens))) break;
+    if (one_x) break;
+    if (p.mode == MODE_EXPERT && (mb0 | mb1 | mb2 | mb3) == 0) break;
   }
 }
 
-// Row steps a unit takes: 4, or STRATA_ROW_STEPS (2, 4, 6 or 8) to tune it.
+// Row steps a unit takes: 4, or STRATA_ROW_STEPS (2 or 4) to tune it.
 inline int row_steps() {
   static const int v = [] {
     const char* e = getenv("STRATA_ROW_STEPS");
     const int r = e ? atoi(e) : 4;
-    return (r == 2 || r == 4 || r == 6 || r == 8) ? r : 4;
+    return (r == 2 || r == 4) ? r : 4;
   }();
   return v;
 }
 
-template <int KIND, bool GLU, bool PAIRED, int TT, int RU>
+template <int KIND, bool GLU, bool PAIRED, int TT, int RU, int LT>
 int launch_direct_ru(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
   const int side = 64 / p.ct;
   p.tt = TT;
@@ -401,19 +551,23 @@ int launch_direct_ru(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream
   if (units > INT32_MAX - kWaves) return STRATA_ERR_SHAPE;
   p.items = (int)units;
   const int grid = (int)((units + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL((direct_decode_kernel<KIND, GLU, PAIRED, TT, RU>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((direct_decode_kernel<KIND, GLU, PAIRED, TT, RU, LT>), dim3(grid), dim3(kThreads), 0, stream, p);
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }
 
+// the row length at compile time for 4096 and 1536 inputs (64 and 32 lanes to a row), at run time otherwise
+template <int KIND, bool GLU, bool PAIRED, int TT, int RU>
+int launch_direct_lt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
+  if (p.ct == 64) return launch_direct_ru<KIND, GLU, PAIRED, TT, RU, 64>(p, grid_y, grid_z, s);
+  if (p.ct == 32) return launch_direct_ru<KIND, GLU, PAIRED, TT, RU, 32>(p, grid_y, grid_z, s);
+  return launch_direct_ru<KIND, GLU, PAIRED, TT, RU, 0>(p, grid_y, grid_z, s);
+}
+
 template <int KIND, bool GLU, bool PAIRED, int TT>
 int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
-  switch (row_steps()) {
-    case 2: return launch_direct_ru<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
-    case 6: return launch_direct_ru<KIND, GLU, PAIRED, TT, 6>(p, grid_y, grid_z, s);
-    case 8: return launch_direct_ru<KIND, GLU, PAIRED, TT, 8>(p, grid_y, grid_z, s);
-    default: return launch_direct_ru<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
-  }
+  if (row_steps() == 2) return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
+  return launch_direct_lt<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
 }
 
 // Rows of 64 to 4096 weights in run pairs (every IQ3_S / IQ3_XXS / Q2_0 row), up to 256 pairs.
@@ -439,7 +593,8 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
   if constexpr (FastTraits<KIND>::supported) {
     if (x_dtype == DT_F16 && out_dtype == DT_F16 && p.row_ids == nullptr) {
       const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
-                                                                     : (glu ? p.pairs <= 16 : p.pairs <= p.share));
+                                                                     : (glu ? p.pairs <= 16
+                                                                            : p.pairs <= p.share || p.pairs <= 8));
       if (p.glu_out != nullptr) {
         if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
