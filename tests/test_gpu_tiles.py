@@ -45,7 +45,10 @@ def test_the_tile_product_is_the_product_with_the_weights(gpu, kind, dtype):
     rng = np.random.default_rng(0)
     shape = (4, 128, 512)
     data, w = stack(kind, rng, *shape)
-    w = w.astype(np.float32 if dtype == torch.float32 else np.float16).astype(np.float64)  # weights as the MFMA takes them
+    # weights as the MFMA takes them: exact for float32 activations and for the codebook types' whole blocks
+    # (float16 integer codes, the run scale on the float32 sums); rounded to float16 otherwise
+    exact = dtype == torch.float32 or (kind in ("IQ3_S", "IQ3_XXS", "Q2_0") and shape[2] % 256 == 0)
+    w = w.astype(np.float32 if exact else np.float16).astype(np.float64)
     tiles = np.array([3, 0, 0, 2, 3])
     a = torch.from_numpy(rng.standard_normal((16 * len(tiles), shape[2])).astype(np.float32)).to(dtype)
     got = B.tile_matmul(dev(data, gpu), kind, shape, a.to(gpu), dev(tiles.astype(np.int32), gpu)).cpu().numpy()
