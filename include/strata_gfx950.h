@@ -110,8 +110,10 @@ int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t ex
 
 /* c[s, :] = W[tile_expert[s / tile]] . a[s, :] for s < n_tiles * tile; a (n_tiles * tile, cols) in
  * a_dtype, c (n_tiles * tile, rows) float32. Tiles naming no expert (>= experts) are skipped and
- * their rows of c are left as they were. F16/BF16 activations multiply weights rounded to float16
- * on MFMA (float32 sums); F32 activations multiply exact weights in float32.
+ * their rows of c are left as they were. F16/BF16 activations go to MFMA as float16 (float32 sums):
+ * IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight blocks multiply exact weights (integer codes, the
+ * run scale applied to the float32 sums), other types weights rounded to float16. F32 activations
+ * multiply exact weights in float32.
  * Replaces tile_matmul + _TILES, strata_mlx/blocks.py:634-654, 583-626. */
 int strata_grouped_matmul(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
                           const void* a, int a_dtype, const uint32_t* tile_expert, int64_t n_tiles, int64_t tile,

@@ -271,8 +271,10 @@ def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, 
 
     a (P, cols), P a multiple of TOKENS_TILE, every TOKENS_TILE rows for one expert; tile_expert (P / 16,) says
     which, or names no expert (>= experts) for a tile to leave out: its rows of the result are then whatever was
-    in memory (in `out` if given). float16/bfloat16 activations multiply weights rounded to float16, float32 ones
-    exact weights; sums are float32. Returns (P, rows) float32. strata_mlx/blocks.py:634-654."""
+    in memory (in `out` if given). float16/bfloat16 activations multiply weights rounded to float16 (exact weights
+    for IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight blocks: their codes are exact in float16 and the run
+    scales multiply the float32 sums), float32 ones exact weights; sums are float32. Returns (P, rows) float32.
+    strata_mlx/blocks.py:634-654."""
     experts, rows, cols = shape
     _flat_u8(blocks)
     a = a.contiguous()
