@@ -119,6 +119,27 @@ int strata_grouped_matmul(int kind, const void* blocks, int64_t experts, int64_t
                           const void* a, int a_dtype, const uint32_t* tile_expert, int64_t n_tiles, int64_t tile,
                           float* c, void* stream);
 
+/* out[t, r] = W[r, :] . x[t, :] for a float16 W (rows x cols, row-major) and `tokens` rows of x
+ * (STRATA_F16 or STRATA_F32); out (tokens, rows) float32. cols must be a multiple of 8. The router's
+ * product, read as the weights are. Replaces WindowLinear + _MATVEC, strata_mlx/fused.py:334-390. */
+int strata_router_matvec(const void* w, int64_t rows, int64_t cols, const void* x, int64_t tokens, int x_dtype,
+                         float* out, void* stream);
+
+/* idx[r, :] = the k largest of logits[r, :] (rows x n float32), largest first, ties to the lower index
+ * (what a stable sort gives); if `weights` is not NULL, weights[r, :] = the softmax of those k logits
+ * (float32). n <= 2048, k <= 64. Replaces top_k + _TOPK and the softmax of _Routed.__call__,
+ * strata_mlx/fused.py:400-436, 490-491. */
+int strata_top_k(const float* logits, int64_t rows, int64_t n, int64_t k, uint32_t* idx, float* weights,
+                 void* stream);
+
+/* out[t, :] = half(sum_j y[t, j, :] * w[t, j]) + half(half(sigmoid(g[t])) * s[t, :]): y (rows, k, d),
+ * g (rows), s and out (rows, d) float16, w (rows, k) float32. The experts are added in the order of the
+ * reference (eight partial sums, expert j into sum j % 8, each product rounded before it is added, then
+ * the sums in order); each float16 operation rounds once. Replaces moe_combine + _COMBINE,
+ * strata_mlx/fused.py:448-481. */
+int strata_moe_combine(const void* y, const float* w, const void* g, const void* s, int64_t rows, int64_t k,
+                       int64_t d, int dtype, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,9 @@ SIGNATURES = {
     "strata_dequant": (_i, [_i, _p, _i64, _i64, _i64, _p, _i, _p]),
     "strata_expert_matvec": (_i, [_i, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _i64, _p, _p]),
     "strata_expert_matvec2": (_i, [_i, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _i64, _p, _p, _p]),
+    "strata_router_matvec": (_i, [_p, _i64, _i64, _p, _i64, _i, _p, _p]),
+    "strata_top_k": (_i, [_p, _i64, _i64, _i64, _p, _p, _p]),
+    "strata_moe_combine": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i, _p, _p]),
     "strata_expert_gate_up_swiglu": (_i, [_i, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _i64, _p, _p, _p, _p]),
     "strata_expert_matvec_swiglu": (_i, [_i, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _i, _p, _p]),
     "strata_expert_matvec_ptrs": (_i, [_i, _p, _i64, _i64, _i64, _p, _i, _i64, _p, _p]),

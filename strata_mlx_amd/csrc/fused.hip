@@ -1,0 +1,216 @@
+// Either side of the expert path: the router's product, its top-k choice with the softmax of the chosen logits,
+// and the combine of the experts' outputs with the shared expert (strata_mlx/fused.py:357-497).
+//
+//   router_matvec  out[t, r] = W[r, :] . x[t, :], W float16 (rows x cols), x float16 / float32, sums float32.
+//                  A wave a row: 64 lanes read the row with 16-byte loads (coalesced), v_dot2 against each
+//                  token's activations, a DPP reduction; HBM-bound (2 MB for 256 x 4096).
+//   top_k          a wave a row of logits: the k largest, ties to the lower index (the order a stable sort
+//                  gives), in descending order; and the softmax of the chosen logits in float32.
+//   moe_combine    out = (half)(sum_k y_k * w_k) + (half)((half)sigmoid(g) * s), the experts added in the order
+//                  of strata_mlx/fused.py:448-466 (eight partial sums, expert j into sum j % 8, each product
+//                  rounded before it is added, the sums in order), every half operation rounded once.
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;  // waves a workgroup
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // lanes ^ 1
+  v += dpp_mov<0x4E>(v);   // lanes ^ 2
+  v += dpp_mov<0x141>(v);  // mirror within 8
+  v += dpp_mov<0x140>(v);  // mirror within 16
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// One wave a row, all tokens (at most 8 a launch; the host splits longer inputs).
+template <typename XT>
+__global__ __launch_bounds__(256) void router_matvec_kernel(const f16* __restrict__ w, int rows, int cols,
+                                                            const XT* __restrict__ x, int tokens,
+                                                            float* __restrict__ out) {
+  const int lane = threadIdx.x % 64;
+  const int row = blockIdx.x * kWaves + threadIdx.x / 64;
+  if (row >= rows) return;
+  const f16* wr = w + (int64_t)row * cols;
+  float acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+  for (int c = lane * 8; c < cols; c += 512) {
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + c);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t < tokens) {
+        if constexpr (sizeof(XT) == 2) {
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(x + (int64_t)t * cols + c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // elements copied out first: a bit cast of a vector element lvalue reads element 0 whatever the index
+            const uint32_t wi = wv[i], xi = xv[i];
+            acc[t] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, wi), __builtin_bit_cast(h2_t, xi), acc[t], false);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t wi = wv[i];
+            const h2_t pw = __builtin_bit_cast(h2_t, wi);
+            acc[t] += (float)pw[0] * x[(int64_t)t * cols + c + 2 * i] + (float)pw[1] * x[(int64_t)t * cols + c + 2 * i + 1];
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t < tokens) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) out[(int64_t)t * rows + row] = v;
+    }
+  }
+}
+
+// (value, index) a over b: larger value, then lower index
+__device__ __forceinline__ bool beats(float va, uint32_t ia, float vb, uint32_t ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// One wave a row of n <= 2048 logits; k <= 64.
+__global__ __launch_bounds__(256) void top_k_kernel(const float* __restrict__ logits, int rows, int n, int k,
+                                                    uint32_t* __restrict__ idx, float* __restrict__ weights) {
+  const int lane = threadIdx.x % 64;
+  const int row = blockIdx.x * kWaves + threadIdx.x / 64;
+  if (row >= rows) return;
+  const float* lr = logits + (int64_t)row * n;
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const int j = i * 64 + lane;
+    v[i] = j < n ? lr[j] : -INFINITY;
+  }
+  float chosen = 0.0f;  // lane q keeps the q-th chosen logit
+  uint32_t taken = 0;
+  for (int q = 0; q < k; ++q) {
+    float best = -INFINITY;
+    uint32_t at = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t j = (uint32_t)(i * 64 + lane);
+      if ((int)j < n && beats(v[i], j, best, at)) {
+        best = v[i];
+        at = j;
+      }
+    }
+    for (int o = 32; o >= 1; o /= 2) {
+      const float ob = __shfl_xor(best, o);
+      const uint32_t oa = (uint32_t)__shfl_xor((int)at, o);
+      if (beats(ob, oa, best, at)) {
+        best = ob;
+        at = oa;
+      }
+    }
+    if (lane == q) {
+      chosen = best;
+      taken = at;
+    }
+    if (at != 0xffffffffu && (int)(at % 64) == lane) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        if (i == (int)(at / 64)) v[i] = -INFINITY;
+    }
+  }
+  if (lane < k) idx[(int64_t)row * k + lane] = taken;
+  if (weights != nullptr) {
+    float m = lane < k ? chosen : -INFINITY;
+    for (int o = 32; o >= 1; o /= 2) m = fmaxf(m, __shfl_xor(m, o));
+    const float ex = lane < k ? expf(chosen - m) : 0.0f;
+    float s = ex;
+    for (int o = 32; o >= 1; o /= 2) s += __shfl_xor(s, o);
+    if (lane < k) weights[(int64_t)row * k + lane] = ex / s;
+  }
+}
+
+// One thread an output element.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const f16* __restrict__ y, const float* __restrict__ w,
+                                                          const f16* __restrict__ g, const f16* __restrict__ s,
+                                                          int k, int d, f16* __restrict__ out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  if (i >= d) return;
+  float acc = 0.0f;
+  for (int j = 0; j < 8 && j < k; ++j) {
+    float part = 0.0f;
+    for (int q = j; q < k; q += 8)
+      part = __fadd_rn(__fmul_rn((float)y[((int64_t)t * k + q) * d + i], w[(int64_t)t * k + q]), part);
+    acc = j == 0 ? part : __fadd_rn(part, acc);
+  }
+  const f16 routed = from_f32<f16>(acc);
+  const f16 gate = from_f32<f16>(1.0f / (1.0f + expf(-(float)g[t])));
+  const f16 shared = from_f32<f16>((float)gate * (float)s[(int64_t)t * d + i]);  // exact product, one rounding
+  out[(int64_t)t * d + i] = routed + shared;                                      // a float16 add: one rounding
+}
+
+}  // namespace
+
+extern "C" {
+
+int strata_router_matvec(const void* w, int64_t rows, int64_t cols, const void* x, int64_t tokens, int x_dtype,
+                         float* out, void* stream) {
+  if (rows < 0 || cols < 0 || tokens < 0) return STRATA_ERR_ARG;
+  if (rows == 0 || tokens == 0) return STRATA_OK;
+  if (!w || !x || !out) return STRATA_ERR_ARG;
+  if (cols % 8 || rows > INT32_MAX / 2 || cols > (1 << 24)) return STRATA_ERR_SHAPE;
+  if (x_dtype != DT_F16 && x_dtype != DT_F32) return STRATA_ERR_DTYPE;
+  const int grid = (int)((rows + kWaves - 1) / kWaves);
+  hipStream_t s = (hipStream_t)stream;
+  for (int64_t t0 = 0; t0 < tokens; t0 += 8) {
+    const int nt = (int)std::min<int64_t>(8, tokens - t0);
+    if (x_dtype == DT_F16)
+      hipLaunchKernelGGL(router_matvec_kernel<f16>, dim3(grid), dim3(256), 0, s, (const f16*)w, (int)rows,
+                         (int)cols, (const f16*)x + t0 * cols, nt, out + t0 * rows);
+    else
+      hipLaunchKernelGGL(router_matvec_kernel<float>, dim3(grid), dim3(256), 0, s, (const f16*)w, (int)rows,
+                         (int)cols, (const float*)x + t0 * cols, nt, out + t0 * rows);
+    STRATA_CHECK_LAUNCH();
+  }
+  return STRATA_OK;
+}
+
+int strata_top_k(const float* logits, int64_t rows, int64_t n, int64_t k, uint32_t* idx, float* weights,
+                 void* stream) {
+  if (rows < 0 || n < 0 || k < 0) return STRATA_ERR_ARG;
+  if (rows == 0 || k == 0) return STRATA_OK;
+  if (!logits || !idx) return STRATA_ERR_ARG;
+  if (n > 2048 || k > 64 || k > n || rows > INT32_MAX / 2) return STRATA_ERR_SHAPE;
+  const int grid = (int)((rows + kWaves - 1) / kWaves);
+  hipLaunchKernelGGL(top_k_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, logits, (int)rows, (int)n, (int)k,
+                     idx, weights);
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
+int strata_moe_combine(const void* y, const float* w, const void* g, const void* s, int64_t rows, int64_t k,
+                       int64_t d, int dtype, void* out, void* stream) {
+  if (rows < 0 || k < 0 || d < 0) return STRATA_ERR_ARG;
+  if (rows == 0 || d == 0) return STRATA_OK;
+  if (!y || !w || !g || !s || !out || k == 0) return STRATA_ERR_ARG;
+  if (dtype != DT_F16) return STRATA_ERR_DTYPE;
+  if (rows > 65535 || d > INT32_MAX / 2) return STRATA_ERR_SHAPE;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((int)((d + 255) / 256), (int)rows), dim3(256), 0, (hipStream_t)stream,
+                     (const f16*)y, w, (const f16*)g, (const f16*)s, (int)k, (int)d, (f16*)out);
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
+}  // extern "C"

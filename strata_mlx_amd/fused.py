@@ -1,0 +1,82 @@
+"""Either side of the expert path: the router, its choice of experts and the combine; strata_mlx/fused.py:334-497
+with torch tensors on the GPU in place of mx.array.
+
+    WindowLinear  a float16 linear layer (the router) whose products come back in float32, read as it is
+    top_k         the k largest logits of each row, ties to the lower index; with `weights`, their softmax
+    moe_combine   sum_k y_k * w_k plus sigmoid(g) * the shared expert, in the reference's order and rounding
+    route         router -> top_k -> softmax, as _Routed.__call__ makes the experts' indices and weights
+"""
+
+import torch
+
+from . import _lib
+
+COMBINE_UPTO = 16  # tokens; strata_mlx/fused.py:468
+
+
+class WindowLinear:
+    """A float16 `nn.Linear` without bias whose products come back in float32; strata_mlx/fused.py:356-390.
+    Up to `upto` tokens of float16 / float32 activations go through the kernel, longer inputs through torch."""
+
+    upto = 8
+
+    def __init__(self, weight: torch.Tensor):
+        if weight.dtype != torch.float16 or weight.ndim != 2:
+            raise ValueError("WindowLinear takes a float16 (rows, cols) weight")
+        _lib.require_device(weight)
+        self.weight = weight.contiguous()
+        self.rows, self.cols = weight.shape
+
+    def takes(self, x: torch.Tensor) -> bool:
+        return x.numel() // self.cols <= self.upto and x.dtype in (torch.float16, torch.float32) and self.cols % 8 == 0
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        if not self.takes(x):
+            return x.float() @ self.weight.float().T
+        tokens = x.numel() // self.cols
+        x2 = x.reshape(tokens, self.cols).contiguous()
+        out = torch.empty((tokens, self.rows), dtype=torch.float32, device=x.device)
+        _lib.check(_lib.library().strata_router_matvec(self.weight.data_ptr(), self.rows, self.cols, x2.data_ptr(),
+                                                         tokens, _lib.dtype_id(x.dtype), out.data_ptr(),
+                                                         _lib.stream()), "router")
+        return out.reshape(*x.shape[:-1], self.rows)
+
+
+def top_k(logits: torch.Tensor, k: int, weights: bool = False):
+    """The indices of the k largest logits (..., N) float32, largest first, ties to the lower index: the order
+    `mx.argpartition(-logits, k - 1)[..., :k]` gives (strata_mlx/fused.py:422-436). With `weights`, also the
+    softmax of those logits (float32), as _Routed.__call__ takes it (fused.py:490-491)."""
+    n = logits.shape[-1]
+    if logits.dtype != torch.float32:
+        raise ValueError("top_k takes float32 logits")
+    rows = logits.numel() // n
+    lg = logits.reshape(rows, n).contiguous()
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((rows, k), dtype=torch.float32, device=logits.device) if weights else None
+    _lib.check(_lib.library().strata_top_k(lg.data_ptr(), rows, n, k, idx.data_ptr(), _lib.ptr(w), _lib.stream()),
+               "top_k")
+    idx = idx.reshape(*logits.shape[:-1], k)
+    return (idx, w.reshape(*logits.shape[:-1], k)) if weights else idx
+
+
+def moe_combine(y: torch.Tensor, w: torch.Tensor, g: torch.Tensor, s: torch.Tensor) -> torch.Tensor | None:
+    """y (..., K, D) half, w (..., K) float32, g (..., 1) half, s (..., D) half -> (..., D), or None where the
+    reference's kernel does not take it (strata_mlx/fused.py:471-481)."""
+    *lead, k, d = y.shape
+    rows = y.numel() // (k * d)
+    if rows > COMBINE_UPTO or y.dtype != torch.float16 or w.dtype != torch.float32 or d % 256:
+        return None
+    out = torch.empty((rows, d), dtype=y.dtype, device=y.device)
+    yy, ww = y.reshape(rows, k, d).contiguous(), w.reshape(rows, k).contiguous()
+    gg, ss = g.reshape(rows).to(torch.float16).contiguous(), s.reshape(rows, d).to(torch.float16).contiguous()
+    _lib.check(_lib.library().strata_moe_combine(yy.data_ptr(), ww.data_ptr(), gg.data_ptr(), ss.data_ptr(), rows, k,
+                                                 d, _lib.dtype_id(y.dtype), out.data_ptr(), _lib.stream()),
+               "moe_combine")
+    return out.reshape(*lead, d)
+
+
+def route(router: WindowLinear, x: torch.Tensor, k: int):
+    """The experts of each token and their weights: (indices (..., k) int32, weights (..., k) float32), as
+    strata_mlx/fused.py:488-491 makes them."""
+    logits = router(x)
+    return top_k(logits, k, weights=True)

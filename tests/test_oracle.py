@@ -355,3 +355,55 @@ def test_the_oracle_still_gives_the_committed_vectors():
     assert np.array_equal(O.swiglu_rounded(g.astype(np.float32), u.astype(np.float32), np.float32),
                           gold["swiglu/h32"])
 
+
+
+# ---- the router, its choice and the combine (oracle/fused.py)
+
+def test_top_k_is_a_brute_force_selection_with_ties_to_the_lower_index():
+    from oracle import fused as OF
+
+    rng = np.random.default_rng(2)
+    logits = rng.integers(-3, 4, (50, 40)).astype(np.float32)  # many ties
+    got = OF.top_k(logits, 7)
+    for r in range(len(logits)):
+        left = list(range(40))
+        for q in range(7):
+            best = max(left, key=lambda j: (logits[r, j], -j))
+            assert got[r, q] == best
+            left.remove(best)
+
+
+def test_softmax_of_the_chosen_has_its_closed_forms():
+    from oracle import fused as OF
+
+    eq = np.zeros((1, 16), np.float32)
+    idx = OF.top_k(eq, 4)
+    assert np.array_equal(idx[0], [0, 1, 2, 3]) and np.allclose(OF.softmax_k(eq, idx), 0.25)
+    far = np.array([[0.0, 200.0, 1.0, -5.0]], np.float32)
+    idx = OF.top_k(far, 3)
+    assert np.array_equal(idx[0], [1, 2, 0]) and OF.softmax_k(far, idx)[0, 0] == 1.0
+
+
+def test_combine_adds_the_experts_in_the_references_order():
+    """fused.py:448-466: experts j, j + 8, ... into partial sum j (each product rounded first), then the partial
+    sums in order. With k = 9, partial sum 0 holds the two tiny products (2^-24 each) and reaches 2^-23 before
+    the product 1 + 2^-11 (a float16 midpoint) is added: 1 + 2^-11 + 2^-23 rounds up to 1 + 2^-10 in float16. A
+    plain left-to-right sum loses each 2^-24 against 1 + 2^-11 and rounds to 1. One-hot weights give y exactly;
+    g = -inf drops the shared expert, g = 0 halves it."""
+    from oracle import fused as OF
+
+    y = np.ones((1, 9, 256), np.float16)
+    w = np.zeros((1, 9), np.float32)
+    w[0, 0] = w[0, 8] = 2.0 ** -24
+    w[0, 1] = 1.0 + 2.0 ** -11
+    s = np.full((1, 256), 3.0, np.float16)
+    out = OF.moe_combine(y, w, np.array([-np.inf], np.float16), s)
+    assert (out == np.float16(1.0 + 2.0 ** -10)).all()
+    rng = np.random.default_rng(1)
+    y = rng.standard_normal((2, 8, 256)).astype(np.float16)
+    onehot = np.zeros((2, 8), np.float32)
+    onehot[0, 5] = onehot[1, 2] = 1.0
+    out = OF.moe_combine(y, onehot, np.array([-np.inf, -np.inf], np.float16), s.repeat(2, 0))
+    assert np.array_equal(out[0], y[0, 5]) and np.array_equal(out[1], y[1, 2])
+    half = OF.moe_combine(np.zeros_like(y), onehot, np.array([0.0, 0.0], np.float16), s.repeat(2, 0))
+    assert (half == np.float16(1.5)).all()
