@@ -86,9 +86,18 @@ __device__ __forceinline__ void load_pair(const uint8_t* row, int j, RunPair<KIN
   }
 }
 
+// The LDS tables of the register decode: codebook entries as four float16 integers, and the XOR masks of four
+// sign bits (16 entries of 8 bytes: one row of banks, so lanes reading different entries never conflict).
+template <int KIND>
+struct DirectTables {
+  u32x2 grid[FastTraits<KIND>::grid > 0 ? FastTraits<KIND>::grid : 1];
+  u32x2 sign4[16];
+  u32x2 q2[FastTraits<KIND>::q2 > 0 ? FastTraits<KIND>::q2 : 1];  // a Q2_0 code byte: four (c - 1)
+};
+
 // run h (0, 1) of a pair: 16 packed float16 pairs of integers, and the run's scale
 template <int KIND>
-__device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint32_t* w, const FastTables<KIND>& t) {
+__device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint32_t* w, const DirectTables<KIND>& t) {
   const float d = half_bits(f.d);
   if constexpr (KIND == K_IQ3_S) {  // strata_mlx/blocks.py:89-102
     const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
@@ -104,9 +113,9 @@ __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       const u32x2 g = t.grid[ix[l]];
-      const u32x4 m = t.signs[(sg >> (8 * (l >> 1))) & 255];
-      w[2 * l] = g[0] ^ m[(l & 1) * 2];
-      w[2 * l + 1] = g[1] ^ m[(l & 1) * 2 + 1];
+      const u32x2 m = t.sign4[(sg >> (4 * l)) & 15];
+      w[2 * l] = g[0] ^ m[0];
+      w[2 * l + 1] = g[1] ^ m[1];
     }
     return scale;
   } else if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116
@@ -116,9 +125,11 @@ __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       const u32x2 g = t.grid[((l < 4 ? qs0 : qs1) >> (8 * (l & 3))) & 255];
-      const u32x4 m = t.signs[(aux >> (7 * (l >> 1))) & 127];
-      w[2 * l] = g[0] ^ m[(l & 1) * 2];
-      w[2 * l + 1] = g[1] ^ m[(l & 1) * 2 + 1];
+      const uint32_t s7 = (aux >> (7 * (l >> 1))) & 127;
+      const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);  // ksigns: the parity in bit 7
+      const u32x2 m = t.sign4[(s8 >> (4 * (l & 1))) & 15];
+      w[2 * l] = g[0] ^ m[0];
+      w[2 * l + 1] = g[1] ^ m[1];
     }
     return scale;
   } else {  // Q2_0, strata_mlx/blocks.py:58-68
@@ -150,7 +161,7 @@ __device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
   }
 }
 template <int KIND>
-__device__ __forceinline__ void store_tables(FastTables<KIND>& t, const TableFetch<KIND>& tf, int tid) {
+__device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableFetch<KIND>& tf, int tid) {
   if constexpr (FastTraits<KIND>::grid > 0) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -161,9 +172,9 @@ __device__ __forceinline__ void store_tables(FastTables<KIND>& t, const TableFet
                           pack_h2((float)((g >> 16) & 255), (float)(g >> 24))};
     }
   }
-  if constexpr (FastTraits<KIND>::signs > 0) {
-    for (int i = tid; i < FastTraits<KIND>::signs; i += kThreads)
-      t.signs[i] = sign_masks(KIND == K_IQ3_XXS ? strata_ksign((uint32_t)i) : (uint32_t)i);
+  if (tid < 16) {
+    const u32x4 m = sign_masks((uint32_t)tid);
+    t.sign4[tid] = u32x2{m[0], m[1]};
   }
   if constexpr (FastTraits<KIND>::q2 > 0) {
     for (int i = tid; i < 256; i += kThreads)
@@ -286,7 +297,7 @@ __device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
 // pairs load the last row / run pair again, and an expert id out of range loads expert 0's rows and writes NaN.
 template <int KIND, bool GLU, bool PAIRED, int TT, int RU, int LT>
 __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kernel(MatvecParams p) {
-  __shared__ FastTables<KIND> tab;
+  __shared__ DirectTables<KIND> tab;
   __shared__ u32x4 xs[kDMaxCols / 8];  // one token's activations, when every wave multiplies the same token
   const int tid = threadIdx.x, lane = tid % 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);

@@ -64,7 +64,7 @@ __device__ __forceinline__ void load_step_acts(const AT* a, const GemmParams& p,
 
 template <int KIND, typename AT>
 __global__ __launch_bounds__(kThreads, 2) void direct_gemm_kernel(GemmParams p) {
-  __shared__ strata_mv::FastTables<KIND> tab;
+  __shared__ strata_mv::DirectTables<KIND> tab;
   __shared__ __attribute__((aligned(16))) f16 w_lds[kDRows * kDPitch];
   __shared__ float s_lds[kDRows * kDRuns];
   __shared__ __attribute__((aligned(16))) f16 a_lds[kDTiles * 16 * kDPitch];
@@ -85,7 +85,11 @@ __global__ __launch_bounds__(kThreads, 2) void direct_gemm_kernel(GemmParams p) 
   for (int i = 1; i < kDTiles; ++i)
     if (t0 + i < wend && nt == i && p.tile_expert[t0 + i] == e) nt = i + 1;
 
-  strata_mv::fast_load_tables<KIND>(tab, tid, kThreads);
+  {
+    strata_mv::TableFetch<KIND> tf;
+    strata_mv::fetch_tables<KIND>(tf, tid);
+    strata_mv::store_tables<KIND>(tab, tf, tid);
+  }
   const uint8_t* mat = p.blocks + (int64_t)e * p.mat_bytes;
   const AT* a = reinterpret_cast<const AT*>(p.a);
   // decode share: row dr, run pair dj of the step
