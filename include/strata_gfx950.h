@@ -140,6 +140,31 @@ int strata_top_k(const float* logits, int64_t rows, int64_t n, int64_t k, uint32
 int strata_moe_combine(const void* y, const float* w, const void* g, const void* s, int64_t rows, int64_t k,
                        int64_t d, int dtype, void* out, void* stream);
 
+/* The Q2_0 table of sums (float16 only). table (tokens, cols / 2, 16) float16: entry c of input pair g of token
+ * t is (c & 3 - 1) * x[t, 2g] + (c >> 2 - 1) * x[t, 2g + 1], summed in float32 and rounded once. Replaces
+ * lookup_table + _TABLE, strata_mlx/blocks.py:718-781. */
+int strata_q2_lookup_table(const void* x, int64_t tokens, int64_t cols, void* table, void* stream);
+
+/* The same table of silu(gate) * up (sigmoid in float32 with expf, nothing rounded before the sums). Replaces
+ * lookup_table_glu + _TABLE_GLU, strata_mlx/blocks.py:728-795. */
+int strata_q2_lookup_table_glu(const void* gate, const void* up, int64_t tokens, int64_t cols, void* table,
+                               void* stream);
+
+/* out[p, r] = W[idx[p], r, :] . x[p / share] for a Q2_0 stack, x given as its table; float16 out (pairs, rows).
+ * per_row lanes a row (a power of two <= 32): lane `part` sums runs part, part + per_row, ... and the row's
+ * total is their sums in lane order, so per_row fixes the bits. With blocks_b / out_b (not NULL), a second stack
+ * of the same shape in the same launch, each row summed as alone (gate and up). cols <= 4096, a multiple of 64.
+ * Replaces lookup_matvec + _LOOKUP and lookup_gate_up + _LOOKUP_TWO, strata_mlx/blocks.py:741-761, 798-852. */
+int strata_q2_lookup_matvec(const void* blocks, const void* blocks_b, int64_t experts, int64_t rows, int64_t cols,
+                            const uint32_t* idx, int64_t pairs, const void* table, int64_t share, int per_row,
+                            void* out, void* out_b, void* stream);
+
+/* strata_q2_lookup_matvec(..., table of strata_q2_lookup_table_glu(gate, up), share 1) in one launch, each pair's
+ * table built in LDS: the same bits. gate, up (pairs, cols) float16. Replaces lookup_down_glu + _DOWN_GLU,
+ * strata_mlx/blocks.py:855-914. */
+int strata_q2_lookup_down_glu(const void* blocks, int64_t experts, int64_t rows, int64_t cols, const uint32_t* idx,
+                              int64_t pairs, const void* gate, const void* up, int per_row, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,8 @@ The blocks go to the GPU as the file's bytes (a uint8 tensor) and hand-written H
     matvec     out[pair, row] = W[expert of pair, row, :] . x     decode: bandwidth-bound, no MFMA
                (also with every pair's expert as an array of its own: matvec_separate)
     window     the same for one layer and a window of tokens (window_matvec, dense.BlockLinear)
+    lookup     Q2_0 over float16 from a table of the 16 sums of each input pair (lookup_table, lookup_matvec,
+               lookup_gate_up, lookup_down_glu)
     tiles      a prompt's pairs sorted by expert into tiles; weights decoded into LDS, MFMA products
     dequant    every weight of the stack as float16 or float32, bit-exact
 
@@ -199,14 +201,138 @@ def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torc
     return out
 
 
+# ---- Q2_0 from a table of sums (strata_mlx/blocks.py:697-928): two weights of a nibble make one of 16 sums of
+# their two inputs; with those sums in a float16 table a code byte costs two table reads. float16 only.
+
+LOOKUP_FROM = 1  # (token, expert) pairs from which Q2_0 experts over float16 go this way (blocks.py:711)
+LOOKUP_MAX_COLS = 4096  # a token's table, 16 * cols bytes, is held in LDS
+
+
+def _threads_per_row(runs: int) -> int:
+    """As many as divide a row evenly and leave each at least four runs (strata_mlx/blocks.py:303-308)."""
+    p = 1
+    while p < 32 and runs % (2 * p) == 0 and runs // (2 * p) >= 4:
+        p *= 2
+    return p
+
+
+def _lookup_per_row(cols: int, pairs: int) -> int:
+    """Lanes a row of lookup_matvec / lookup_gate_up: strata_mlx/blocks.py:797-803."""
+    per_row = _threads_per_row(cols // 32)
+    if cols >= 2048:
+        per_row = min(per_row, 8 if pairs <= 40 else 2)
+    elif pairs > 20:
+        per_row = min(per_row, 4)
+    return per_row
+
+
+def lookable(lin, dtype: torch.dtype) -> bool:
+    """strata_mlx/blocks.py:764-765, and rows whose table fits LDS."""
+    return lin.kind == "Q2_0" and dtype == torch.float16 and lin.input_dims <= LOOKUP_MAX_COLS
+
+
+def lookup_table(x: torch.Tensor) -> torch.Tensor:
+    """x (n, cols) float16 -> (n, cols / 2, 16): for every two inputs, the sums two weights can make of them.
+    strata_mlx/blocks.py:768-777."""
+    if x.dtype != torch.float16:
+        raise ValueError("lookup_table takes float16 activations")
+    _lib.require_device(x)
+    n, cols = x.shape
+    x = x.contiguous()
+    table = torch.empty((n, cols // 2, 16), dtype=torch.float16, device=x.device)
+    _lib.check(_lib.library().strata_q2_lookup_table(x.data_ptr(), n, cols, table.data_ptr(), _lib.stream()),
+               "lookup_table")
+    return table
+
+
+def lookup_table_glu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """The table of silu(gate) * up, both (n, cols) float16. strata_mlx/blocks.py:780-789."""
+    if gate.dtype != torch.float16 or up.dtype != torch.float16 or gate.shape != up.shape:
+        raise ValueError("lookup_table_glu takes float16 gate and up of one shape")
+    n, cols = gate.shape
+    gate, up = gate.contiguous(), up.contiguous()
+    table = torch.empty((n, cols // 2, 16), dtype=torch.float16, device=gate.device)
+    _lib.check(_lib.library().strata_q2_lookup_table_glu(gate.data_ptr(), up.data_ptr(), n, cols, table.data_ptr(),
+                                                         _lib.stream()), "lookup_table_glu")
+    return table
+
+
+def _lookup(lins: tuple, idx: torch.Tensor, table: torch.Tensor, share: int) -> tuple:
+    lin = lins[0]
+    if any(not lookable(l, torch.float16) for l in lins) or table.dtype != torch.float16:
+        raise ValueError("the table path takes Q2_0 stacks of at most "
+                         f"{LOOKUP_MAX_COLS} inputs and a float16 table")
+    idx = _idx32(idx)
+    pairs = idx.numel()
+    outs = [torch.empty((pairs, lin.output_dims), dtype=torch.float16, device=table.device) for _ in lins]
+    b = lins[1].blocks.data_ptr() if len(lins) > 1 else None
+    ob = outs[1].data_ptr() if len(lins) > 1 else None
+    _lib.check(_lib.library().strata_q2_lookup_matvec(
+        lin.blocks.data_ptr(), b, lin.num_experts, lin.output_dims, lin.input_dims, idx.data_ptr(), pairs,
+        table.contiguous().data_ptr(), share, _lookup_per_row(lin.input_dims, pairs), outs[0].data_ptr(), ob,
+        _lib.stream()), "lookup_matvec")
+    return tuple(outs)
+
+
+def lookup_matvec(lin, idx: torch.Tensor, table: torch.Tensor, share: int) -> torch.Tensor:
+    """out[pair] = W[idx[pair]] . x[pair / share], x given as its `lookup_table`. Returns (pairs, rows) float16.
+    strata_mlx/blocks.py:792-812."""
+    return _lookup((lin,), idx, table, share)[0]
+
+
+def lookup_gate_up(gate, up, idx: torch.Tensor, table: torch.Tensor, share: int) -> tuple:
+    """(`lookup_matvec(gate, ...)`, `lookup_matvec(up, ...)`) in one launch, the same bits; gate and up of one shape.
+    strata_mlx/blocks.py:829-848."""
+    if (gate.num_experts, gate.output_dims, gate.input_dims) != (up.num_experts, up.output_dims, up.input_dims):
+        raise ValueError("lookup_gate_up takes gate and up of one shape")
+    return _lookup((gate, up), idx, table, share)
+
+
+def lookup_down_glu(lin, idx: torch.Tensor, gate: torch.Tensor, up: torch.Tensor):
+    """`lookup_matvec(lin, idx, lookup_table_glu(gate, up), 1)` in one launch (the same bits), or None where a
+    pair's table does not fit LDS. strata_mlx/blocks.py:889-914."""
+    if not lookable(lin, gate.dtype) or up.dtype != torch.float16:
+        return None
+    idx = _idx32(idx)
+    pairs = idx.numel()
+    # lookup_matvec's lanes a row, so that the two give the same bits. The reference's own rule for down
+    # (blocks.py:893-895) leaves out the rule for rows of 2048 inputs or more; below 2048, where down's rows are,
+    # the two rules agree.
+    per_row = _lookup_per_row(lin.input_dims, pairs)
+    gate = gate.reshape(pairs, lin.input_dims).contiguous()
+    up = up.reshape(pairs, lin.input_dims).contiguous()
+    out = torch.empty((pairs, lin.output_dims), dtype=torch.float16, device=gate.device)
+    _lib.check(_lib.library().strata_q2_lookup_down_glu(
+        lin.blocks.data_ptr(), lin.num_experts, lin.output_dims, lin.input_dims, idx.data_ptr(), pairs,
+        gate.data_ptr(), up.data_ptr(), per_row, out.data_ptr(), _lib.stream()), "lookup_down_glu")
+    return out
+
+
+def _lookup_glu(x: torch.Tensor, indices: torch.Tensor, up, gate, down) -> torch.Tensor:
+    """strata_mlx/blocks.py:917-928: one table for gate and up, gate and up in one launch, down building the table
+    of silu(gate) * up itself."""
+    k = indices.shape[-1] if indices.ndim else 1
+    idx = _idx32(indices)
+    table = lookup_table(x.reshape(-1, x.shape[-1]))
+    if (gate.output_dims, gate.input_dims, gate.num_experts) == (up.output_dims, up.input_dims, up.num_experts):
+        g, u = lookup_gate_up(gate, up, idx, table, k)
+    else:
+        g, u = lookup_matvec(gate, idx, table, k), lookup_matvec(up, idx, table, k)
+    out = lookup_down_glu(down, idx, g, u)
+    if out is None:
+        out = lookup_matvec(down, idx, lookup_table_glu(g, u), 1)
+    return out.reshape(*indices.shape, down.output_dims)
+
+
 def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, gate: BlockSwitchLinear,
                down: BlockSwitchLinear) -> torch.Tensor:
     """down(silu(gate(x)) * up(x)) through each token's experts: x (..., in), indices (..., k) -> (..., k, out).
     The argument order is the reference's (x, indices, up, gate, down); strata_mlx/blocks.py:958-986.
 
     Decode windows take the matvec kernels: gate and up in one launch reading x once and writing silu(gate) * up
-    (rounded as mlx-lm rounds it), then down on that. Prompt chunks (from TILES_FROM pairs) take the
-    tiles: the pairs sorted by expert on the GPU, weights decoded into LDS and multiplied on MFMA."""
+    (rounded as mlx-lm rounds it), then down on that. Q2_0 stacks over float16 take the table of sums, as the
+    reference's do (blocks.py:963-964). Prompt chunks (from TILES_FROM pairs) take the tiles: the pairs sorted by
+    expert on the GPU, weights decoded into LDS and multiplied on MFMA."""
     indices = torch.as_tensor(indices, device=x.device)
     k = indices.shape[-1] if indices.ndim else 1
     flat = indices.reshape(-1)
@@ -214,6 +340,8 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, ga
     if flat.numel() >= TILES_FROM and all(tileable(lin.kind, lin.output_dims, lin.input_dims)
                                           for lin in (up, gate, down)):
         return _tiled_glu(x, indices, up, gate, down)
+    if flat.numel() >= LOOKUP_FROM and all(lookable(lin, x.dtype) for lin in (up, gate, down)):
+        return _lookup_glu(x, indices, up, gate, down)
     if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) == (up.kind, up.output_dims, up.input_dims,
                                                                              up.num_experts):
         _, _, h = gate_up_swiglu(gate, up, xs, flat, k)

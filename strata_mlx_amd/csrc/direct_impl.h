@@ -577,7 +577,9 @@ int launch_direct_lt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
 
 template <int KIND, bool GLU, bool PAIRED, int TT>
 int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
-  if (row_steps() == 2) return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
+  // Q2_0 at two tokens a pass spills at four row steps (the compiler keeps more of its light decode in flight);
+  // two steps give the same sums (each step's lanes meet by the same exchange)
+  if (row_steps() == 2 || (KIND == K_Q2_0 && TT > 1)) return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
   return launch_direct_lt<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
 }
 

@@ -11,6 +11,8 @@
 - Field-by-field checks of IQ3_S / IQ3_XXS / IQ4_XS: one field changed at a time moves exactly the weights it
   should, by exactly the factor it should.
 - tiles_of's invariants (tests/test_blocks.py:177-195 of the reference).
+- The Q2_0 table of sums: its closed form; on exact inputs the table path is the pinned float64 product rounded
+  once; on random inputs within the table's float16 rounding; the lanes of a row only reorder its sum.
 - The committed vectors of tests/golden/ (the oracle's own output at a fixed seed) are reproduced bit for bit.
 """
 
@@ -407,3 +409,76 @@ def test_combine_adds_the_experts_in_the_references_order():
     assert np.array_equal(out[0], y[0, 5]) and np.array_equal(out[1], y[1, 2])
     half = OF.moe_combine(np.zeros_like(y), onehot, np.array([0.0, 0.0], np.float16), s.repeat(2, 0))
     assert (half == np.float16(1.5)).all()
+
+
+# ---- the Q2_0 table of sums (oracle/lookup.py)
+
+def _q2_exact_stack(rng, experts, rows, cols):
+    """Q2_0 blocks whose scales are powers of two: with activations that are integers over four, every sum of the
+    table path is exact in float32 and float16."""
+    data = O.random_blocks("Q2_0", experts * rows * cols // 64, rng).reshape(-1, 18)
+    d = (2.0 ** -rng.integers(0, 4, len(data))) * rng.choice([-1.0, 1.0], len(data))
+    data[:, :2] = d.astype("<f2").reshape(-1, 1).view(np.uint8)
+    return data.reshape(-1)
+
+
+def test_the_table_has_its_closed_form():
+    from oracle import lookup as LK
+
+    rng = np.random.default_rng(5)
+    x = (rng.integers(-40, 41, (3, 64)) / 4).astype(np.float16)
+    t = LK.lookup_table(x)
+    assert t.shape == (3, 32, 16) and t.dtype == np.float16
+    for c in range(16):
+        want = ((c & 3) - 1) * x[:, 0::2].astype(np.float64) + ((c >> 2) - 1) * x[:, 1::2].astype(np.float64)
+        assert np.array_equal(t[:, :, c].astype(np.float64), want)
+    # the table of silu(g) * u is the table of those values
+    g, u = rng.standard_normal((2, 3, 64)).astype(np.float16)
+    h = (g.astype(np.float32) / (1 + np.exp(-g.astype(np.float32))) * u.astype(np.float32)).astype(np.float32)
+    glu = LK.lookup_table_glu(g, u)
+    for c in range(16):
+        want = (np.float32((c & 3) - 1) * h[:, 0::2] + np.float32((c >> 2) - 1) * h[:, 1::2]).astype(np.float16)
+        assert np.array_equal(glu[:, :, c], want)
+
+
+@pytest.mark.parametrize("rows,cols,share,per_row", [(8, 64, 1, 1), (5, 640, 2, 4), (3, 2048, 4, 8), (2, 4096, 8, 32)])
+def test_lookup_on_exact_values_is_the_product_of_the_weights(rows, cols, share, per_row):
+    """Exact inputs: every sum of the table path is exact, so it gives the float64 product of the decoded weights
+    rounded once to float16, bit for bit."""
+    from oracle import lookup as LK
+
+    rng = np.random.default_rng(rows + cols)
+    experts, pairs = 3, 2 * share
+    data = _q2_exact_stack(rng, experts, rows, cols)
+    w = O.dequantize(data, "Q2_0", (experts, rows, cols))
+    idx = rng.integers(0, experts, pairs)
+    x = (rng.integers(-12, 13, (pairs // share, cols)) / 4).astype(np.float16)
+    got = LK.lookup_matvec(data, (experts, rows, cols), idx, LK.lookup_table(x), share, per_row)
+    want = O.expert_matvec(w, idx, x.astype(np.float64), share)
+    assert np.array_equal(got, want.astype(np.float16))
+
+
+def test_lookup_on_random_values_is_the_product_within_the_tables_rounding():
+    from oracle import lookup as LK
+
+    rng = np.random.default_rng(11)
+    experts, rows, cols, pairs = 4, 24, 1024, 6
+    data = O.random_blocks("Q2_0", experts * rows * cols // 64, rng)
+    w = O.dequantize(data, "Q2_0", (experts, rows, cols))
+    idx = rng.integers(0, experts, pairs)
+    x = rng.standard_normal((pairs, cols)).astype(np.float16)
+    got = LK.lookup_matvec(data, (experts, rows, cols), idx, LK.lookup_table(x), 1, 8).astype(np.float64)
+    want = O.expert_matvec(w, idx, x.astype(np.float64), 1)
+    err = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert 1e-5 < err < 2e-3  # the sums' float16 rounding, and no more
+
+
+def test_the_lanes_of_a_row_only_reorder_its_sum():
+    from oracle import lookup as LK
+
+    rng = np.random.default_rng(2)
+    data = _q2_exact_stack(rng, 2, 4, 1024)
+    idx, x = np.array([1, 0]), (rng.integers(-8, 9, (2, 1024)) / 4).astype(np.float16)
+    table = LK.lookup_table(x)
+    outs = [LK.lookup_matvec(data, (2, 4, 1024), idx, table, 1, p) for p in (1, 2, 8, 32)]
+    assert all(np.array_equal(o, outs[0]) for o in outs)
