@@ -165,6 +165,26 @@ int strata_q2_lookup_matvec(const void* blocks, const void* blocks_b, int64_t ex
 int strata_q2_lookup_down_glu(const void* blocks, int64_t experts, int64_t rows, int64_t cols, const uint32_t* idx,
                               int64_t pairs, const void* gate, const void* up, int per_row, void* out, void* stream);
 
+/* Q3_K held as planes: a (rows, cols) Q3_K tensor's blocks rearranged once into hm (blocks x 8 uint32: the 32
+ * high-bit bytes), qs (blocks x 16 uint32: the 64 value bytes), sc (blocks x 16 int8: the 6-bit scales decoded,
+ * less 32) and dd (blocks float16: d), blocks = rows * cols / 256. Replaces q3k_planes,
+ * strata_mlx/blocks.py:397-414. */
+int strata_q3k_planes(const void* blocks, int64_t rows, int64_t cols, uint32_t* hm, uint32_t* qs, int8_t* sc,
+                      void* dd, void* stream);
+
+/* out[t, r] = W[r, :] . x[t, :] for up to 8 tokens of x (STRATA_F32 / F16 / BF16), W as planes; out (tokens,
+ * rows) in x's type. per_row lanes a row (a power of two <= 64) fix the sums' order: chosen by the tensor's shape,
+ * a token gets the same bits alone as in a window. Replaces q3k_planes_window + _Q3K_PLANES_WINDOW,
+ * strata_mlx/blocks.py:425-501. */
+int strata_q3k_planes_window(const uint32_t* hm, const uint32_t* qs, const int8_t* sc, const void* dd, int64_t rows,
+                             int64_t cols, const void* x, int64_t tokens, int x_dtype, int per_row, void* out,
+                             void* stream);
+
+/* Every weight of a tensor held as planes, (rows, cols) float32 / float16, bit-exact. Replaces
+ * q3k_planes_dequantize + _Q3K_PLANES_DEQUANT, strata_mlx/blocks.py:464-512. */
+int strata_q3k_planes_dequant(const uint32_t* hm, const uint32_t* qs, const int8_t* sc, const void* dd, int64_t rows,
+                              int64_t cols, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

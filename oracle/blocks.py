@@ -321,3 +321,32 @@ def tile_matmul(w: np.ndarray, a: np.ndarray, tile_expert: np.ndarray, round_to=
         if e < experts:
             out[t * tile:(t + 1) * tile] = a[t * tile:(t + 1) * tile].astype(np.float64) @ wf[e].T
     return out
+
+
+# ---- Q3_K held as planes (strata_mlx/blocks.py:397-512)
+
+def q3k_planes(data: np.ndarray, rows: int, cols: int) -> dict:
+    """The planes of a Q3_K tensor's bytes: hm (blocks, 8) uint32, qs (blocks, 16) uint32, sc (blocks, 16) int8
+    (the 6-bit scales decoded, less 32), dd (blocks,) float16. strata_mlx/blocks.py:403-414."""
+    b = np.asarray(data, np.uint8).reshape(-1, 110)[: rows * cols // 256]
+    sc = np.stack([_q3k_scale(b[:, 96:108], k) for k in range(16)], axis=1).astype(np.int8)
+    return {"hm": np.ascontiguousarray(b[:, 0:32]).view("<u4").copy(),
+            "qs": np.ascontiguousarray(b[:, 32:96]).view("<u4").copy(),
+            "sc": sc,
+            "dd": np.ascontiguousarray(b[:, 108:110]).view("<f2")[:, 0].copy()}
+
+
+def q3k_planes_weights(planes: dict, rows: int, cols: int) -> np.ndarray:
+    """The weights the planes give by the planes' own formula (strata_mlx/blocks.py:419-422, 464-479): weight
+    4w + k of run rr = 4n + j is d * sc[2rr + (w >= 4)] * (((qs[8n + w] >> (8k + 2j)) & 3) - (bit 8k + rr of
+    hm[w] ? 0 : 4)); float32."""
+    hm, qs = planes["hm"].astype(np.int64), planes["qs"].astype(np.int64)
+    sc, d = planes["sc"].astype(np.float64), planes["dd"].astype(np.float64)
+    out = np.empty((len(d), 8, 32))
+    for rr in range(8):
+        n, j = divmod(rr, 4)
+        for w in range(8):
+            for k in range(4):
+                v = ((qs[:, 8 * n + w] >> (8 * k + 2 * j)) & 3) - np.where((hm[:, w] >> (8 * k + rr)) & 1, 0, 4)
+                out[:, rr, 4 * w + k] = d * sc[:, 2 * rr + (w >= 4)] * v
+    return out.reshape(rows, cols).astype(np.float32)

@@ -7,6 +7,7 @@ The blocks go to the GPU as the file's bytes (a uint8 tensor) and hand-written H
     window     the same for one layer and a window of tokens (window_matvec, dense.BlockLinear)
     lookup     Q2_0 over float16 from a table of the 16 sums of each input pair (lookup_table, lookup_matvec,
                lookup_gate_up, lookup_down_glu)
+    planes     Q3_K rearranged once into aligned planes (q3k_planes, q3k_planes_window, q3k_planes_dequantize)
     tiles      a prompt's pairs sorted by expert into tiles; weights decoded into LDS, MFMA products
     dequant    every weight of the stack as float16 or float32, bit-exact
 
@@ -198,6 +199,65 @@ def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torc
         _lib.kind_id(kind), blocks.data_ptr(), rows, cols, x2.data_ptr(), tokens, _lib.dtype_id(x.dtype),
         out.data_ptr(), _lib.dtype_id(out_dtype), _lib.ptr(ids), n if ids is not None else 0, _lib.stream()),
         f"window {kind}")
+    return out
+
+
+# ---- Q3_K held as planes (strata_mlx/blocks.py:397-512): the blocks rearranged once into aligned arrays of their
+# parts (high-bit words, value words, decoded scales, d), 114 bytes a block where the file has 110.
+
+Q3K_PLANE_BYTES = 114
+PLANES_MAX_TOKENS = 8  # tokens a launch of the planes window kernel takes; more go 8 at a time
+
+
+def q3k_planes(blocks: torch.Tensor, rows: int, cols: int) -> dict:
+    """A Q3_K tensor's blocks (rows, cols as the file has them) -> its planes, on the GPU. strata_mlx/blocks.py:403-414."""
+    _flat_u8(blocks)
+    if cols % 256 or blocks.numel() < rows * row_bytes("Q3_K", cols):
+        raise ValueError(f"Q3_K planes: blocks of a ({rows}, {cols}) tensor")
+    n = rows * cols // 256
+    dev = blocks.device
+    planes = {"hm": torch.empty(n * 8, dtype=torch.int32, device=dev),
+              "qs": torch.empty(n * 16, dtype=torch.int32, device=dev),
+              "sc": torch.empty(n * 16, dtype=torch.int8, device=dev),
+              "dd": torch.empty(n, dtype=torch.float16, device=dev)}
+    _lib.check(_lib.library().strata_q3k_planes(blocks.data_ptr(), rows, cols, planes["hm"].data_ptr(),
+                                                planes["qs"].data_ptr(), planes["sc"].data_ptr(),
+                                                planes["dd"].data_ptr(), _lib.stream()), "q3k_planes")
+    return planes
+
+
+def _planes_per_row(rows: int, cols: int) -> int:
+    """Lanes a row by the tensor's shape, never by the window (strata_mlx/blocks.py:486-490)."""
+    per_row = 2
+    while per_row < 16 and rows * per_row < 20480 and (2 * cols // 256) // (2 * per_row) >= 1:
+        per_row *= 2
+    return per_row
+
+
+def q3k_planes_window(planes: dict, rows: int, cols: int, x: torch.Tensor) -> torch.Tensor:
+    """out[t] = W . x[t] for a Q3_K tensor held as planes, x (tokens, cols). Returns (tokens, rows) in x's type.
+    strata_mlx/blocks.py:482-501."""
+    x = x.reshape(-1, cols).contiguous()
+    tokens = x.shape[0]
+    out = torch.empty((tokens, rows), dtype=x.dtype, device=x.device)
+    per_row = _planes_per_row(rows, cols)
+    for t0 in range(0, tokens, PLANES_MAX_TOKENS):
+        t1 = min(tokens, t0 + PLANES_MAX_TOKENS)
+        _lib.check(_lib.library().strata_q3k_planes_window(
+            planes["hm"].data_ptr(), planes["qs"].data_ptr(), planes["sc"].data_ptr(), planes["dd"].data_ptr(),
+            rows, cols, x[t0:t1].data_ptr(), t1 - t0, _lib.dtype_id(x.dtype), per_row, out[t0:t1].data_ptr(),
+            _lib.stream()), "q3k_planes_window")
+    return out
+
+
+def q3k_planes_dequantize(planes: dict, rows: int, cols: int, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Every weight of a tensor held as planes, bit-exact (float32 / float16). strata_mlx/blocks.py:504-512."""
+    if dtype not in (torch.float32, torch.float16):
+        raise ValueError("q3k_planes_dequantize gives float32 or float16")
+    out = torch.empty((rows, cols), dtype=dtype, device=planes["dd"].device)
+    _lib.check(_lib.library().strata_q3k_planes_dequant(
+        planes["hm"].data_ptr(), planes["qs"].data_ptr(), planes["sc"].data_ptr(), planes["dd"].data_ptr(), rows,
+        cols, out.data_ptr(), _lib.dtype_id(dtype), _lib.stream()), "q3k_planes_dequantize")
     return out
 
 

@@ -4,7 +4,8 @@
                    are packed back into the file's Q6_K blocks once, on the GPU, and every product reads those
                    210-byte blocks (6.56 bits a weight, where the parts take 8.56).
     BlockLinear    a layer kept as the file's blocks, any type the kernels decode (dense.py:205-242); `inputs`
-                   reorders the activations as the reference's does.
+                   reorders the activations as the reference's does. Q3_K layers are held as planes
+                   (blocks.q3k_planes), as the reference holds them.
     BlockEmbedding rows of an embedding decoded when their tokens come (dense.py:245-258).
 
 Up to MAX_TOKENS tokens a product is a window of the matvec kernel (each block decoded once for every token); a
@@ -16,6 +17,7 @@ import torch
 from . import blocks as B
 
 MAX_TOKENS = 8  # more than a window: a chunk of a prompt, multiplied as floats (dense.py:33)
+PLANES = True  # Q3_K layers held as planes (blocks.q3k_planes), as the reference holds them (dense.py:190, 214-215)
 
 
 def q6k_blocks(codes: torch.Tensor, scales: torch.Tensor, d: torch.Tensor) -> torch.Tensor:
@@ -51,15 +53,23 @@ class BlockLinear:
         self.to_file = None
         if inputs is not None:
             self.to_file = torch.argsort(torch.as_tensor(inputs, device=blocks.device)).to(torch.int64)
+        self.planes = None
+        if kind == "Q3_K" and PLANES:  # held as planes instead: aligned words for the window kernel
+            self.planes, self.blocks = B.q3k_planes(blocks, *shape), None
 
     @property
     def nbytes(self) -> int:
+        if self.planes is not None:
+            return sum(a.numel() * a.element_size() for a in self.planes.values())
         return self.blocks.numel()
 
     def floats(self, dtype: torch.dtype) -> torch.Tensor:
         """The weights (out, in), each exact in float32 and rounded once to `dtype`."""
-        w = B.dequantize(self.blocks, self.kind, (self.output_dims, self.input_dims),
-                         torch.float16 if dtype == torch.float16 else torch.float32)
+        half = torch.float16 if dtype == torch.float16 else torch.float32
+        if self.planes is not None:
+            w = B.q3k_planes_dequantize(self.planes, self.output_dims, self.input_dims, half)
+        else:
+            w = B.dequantize(self.blocks, self.kind, (self.output_dims, self.input_dims), half)
         return w if w.dtype == dtype else w.to(dtype)
 
     def __call__(self, x: torch.Tensor, row_ids: torch.Tensor | None = None) -> torch.Tensor:
@@ -69,7 +79,14 @@ class BlockLinear:
         if self.to_file is not None:
             x2 = x2[:, self.to_file]
         tokens = x2.shape[0]
-        if tokens <= MAX_TOKENS or row_ids is not None:
+        if self.planes is not None:
+            if tokens <= MAX_TOKENS:
+                out = B.q3k_planes_window(self.planes, rows, cols, x2)
+            else:
+                out = x2 @ self.floats(x.dtype).T
+            if row_ids is not None:
+                out = out[:, row_ids.reshape(-1).long()]
+        elif tokens <= MAX_TOKENS or row_ids is not None:
             out = B.window_matvec(self.blocks, self.kind, rows, cols, x2, row_ids=row_ids)
         else:
             out = x2 @ self.floats(x.dtype).T

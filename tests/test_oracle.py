@@ -482,3 +482,15 @@ def test_the_lanes_of_a_row_only_reorder_its_sum():
     table = LK.lookup_table(x)
     outs = [LK.lookup_matvec(data, (2, 4, 1024), idx, table, 1, p) for p in (1, 2, 8, 32)]
     assert all(np.array_equal(o, outs[0]) for o in outs)
+
+
+def test_q3k_planes_give_the_weights_of_the_blocks():
+    """The planes' own formula on the rearranged parts gives what the pinned Q3_K decoder gives on the blocks."""
+    rng = np.random.default_rng(8)
+    rows, cols = 6, 768
+    data = O.random_blocks("Q3_K", rows * cols // 256, rng)
+    planes = O.q3k_planes(data, rows, cols)
+    assert planes["hm"].shape == (18, 8) and planes["qs"].shape == (18, 16) and planes["sc"].shape == (18, 16)
+    assert planes["sc"].min() >= -32 and planes["sc"].max() <= 31
+    got = O.q3k_planes_weights(planes, rows, cols)
+    assert np.array_equal(got, O.dequantize(data, "Q3_K", (rows, cols)))
