@@ -172,8 +172,8 @@ int strata_q2_lookup_down_glu(const void* blocks, int64_t experts, int64_t rows,
 int strata_q3k_planes(const void* blocks, int64_t rows, int64_t cols, uint32_t* hm, uint32_t* qs, int8_t* sc,
                       void* dd, void* stream);
 
-/* out[t, r] = W[r, :] . x[t, :] for up to 8 tokens of x (STRATA_F32 / F16 / BF16), W as planes; out (tokens,
- * rows) in x's type. per_row lanes a row (a power of two <= 64) fix the sums' order: chosen by the tensor's shape,
+/* out[t, r] = W[r, :] . x[t, :] for up to 8 tokens of x (STRATA_F32 / F16 / BF16; at most 48 KB of them), W as
+ * planes; out (tokens, rows) in x's type. per_row lanes a row (a power of two <= 64) fix the sums' order: chosen by the tensor's shape,
  * a token gets the same bits alone as in a window. Replaces q3k_planes_window + _Q3K_PLANES_WINDOW,
  * strata_mlx/blocks.py:425-501. */
 int strata_q3k_planes_window(const uint32_t* hm, const uint32_t* qs, const int8_t* sc, const void* dd, int64_t rows,

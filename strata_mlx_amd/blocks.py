@@ -207,6 +207,7 @@ def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torc
 
 Q3K_PLANE_BYTES = 114
 PLANES_MAX_TOKENS = 8  # tokens a launch of the planes window kernel takes; more go 8 at a time
+PLANES_MAX_X_BYTES = 48 * 1024  # and at most this much of their activations (staged in LDS)
 
 
 def q3k_planes(blocks: torch.Tensor, rows: int, cols: int) -> dict:
@@ -227,9 +228,11 @@ def q3k_planes(blocks: torch.Tensor, rows: int, cols: int) -> dict:
 
 
 def _planes_per_row(rows: int, cols: int) -> int:
-    """Lanes a row by the tensor's shape, never by the window (strata_mlx/blocks.py:486-490)."""
-    per_row = 2
-    while per_row < 16 and rows * per_row < 20480 and (2 * cols // 256) // (2 * per_row) >= 1:
+    """Lanes a row by the tensor's shape, never by the window, so that a token gets the same bits alone as in a
+    window (strata_mlx/blocks.py:484-490): here as many as a row has half blocks, up to 16, since a wave of 64
+    lanes and 256 CUs want more lanes than the reference's rule (2 for 10,240 rows) gives."""
+    per_row, halves = 1, 2 * cols // 256
+    while per_row < 16 and per_row < halves:
         per_row *= 2
     return per_row
 
@@ -241,8 +244,9 @@ def q3k_planes_window(planes: dict, rows: int, cols: int, x: torch.Tensor) -> to
     tokens = x.shape[0]
     out = torch.empty((tokens, rows), dtype=x.dtype, device=x.device)
     per_row = _planes_per_row(rows, cols)
-    for t0 in range(0, tokens, PLANES_MAX_TOKENS):
-        t1 = min(tokens, t0 + PLANES_MAX_TOKENS)
+    step = max(1, min(PLANES_MAX_TOKENS, PLANES_MAX_X_BYTES // (cols * x.element_size())))
+    for t0 in range(0, tokens, step):
+        t1 = min(tokens, t0 + step)
         _lib.check(_lib.library().strata_q3k_planes_window(
             planes["hm"].data_ptr(), planes["qs"].data_ptr(), planes["sc"].data_ptr(), planes["dd"].data_ptr(),
             rows, cols, x[t0:t1].data_ptr(), t1 - t0, _lib.dtype_id(x.dtype), per_row, out[t0:t1].data_ptr(),

@@ -10,11 +10,12 @@
 // d * sc[2 rr + (w >= 4)] * (((qs[8 n + w] >> (8 k + 2 j)) & 3) - ((hm[w] >> (8 k + rr)) & 1 ? 0 : 4)).
 //
 //   q3k_planes_kernel   one thread a block: the planes from the file's block (strata_mlx/blocks.py:403-414)
-//   q3k_window_kernel   out[t, r] = W[r, :] . x[t, :] for up to 8 tokens: P lanes a row, lane `part` taking half
-//                       blocks part, part + P, ...; a run's two halves of 16 weights summed apart (four-weight
-//                       dot products in order), then d * sc of each added to the lane's sums; the row's lanes by a
-//                       butterfly. P depends on the tensor's shape only, so a token gets the same bits alone as in
-//                       a window (strata_mlx/blocks.py:425-461, 482-501).
+//   q3k_window_kernel   out[t, r] = W[r, :] . x[t, :] for up to 8 tokens (48 KB of activations, staged in LDS
+//                       once a workgroup): P lanes a row, lane `part` taking half blocks part, part + P, ...; a
+//                       run's two halves of 16 weights summed apart (four-weight dot products in order), then
+//                       d * sc of each added to the lane's sums; the row's lanes by a butterfly. P depends on the
+//                       tensor's shape only, so a token gets the same bits alone as in a window
+//                       (strata_mlx/blocks.py:425-461, 482-501).
 //   q3k_dequant_kernel  one thread a run of 32: (d * sc) * value, exact in float32 (blocks.py:464-479, 504-512).
 // The window kernel is HBM-bound: 114 bytes per 256 weights per row, read once for every token of the window.
 #include <algorithm>
@@ -26,6 +27,7 @@ namespace {
 
 constexpr int kPThreads = 256;
 constexpr int kPMaxTokens = 8;
+constexpr size_t kPMaxXBytes = 48 * 1024;  // a launch's activations, staged in LDS
 
 __global__ __launch_bounds__(kPThreads) void q3k_planes_kernel(const uint8_t* __restrict__ blocks, int64_t n_blocks,
                                                                uint32_t* __restrict__ hm, uint32_t* __restrict__ qs,
@@ -56,28 +58,37 @@ struct PlanesParams {
   int rows, cols, tokens, per_row;
 };
 
+// A workgroup: 256 / P rows, its tokens' activations staged once in LDS in their own type.
 template <typename XT>
 __global__ __launch_bounds__(kPThreads) void q3k_window_kernel(PlanesParams p) {
-  const int gtid = blockIdx.x * kPThreads + threadIdx.x;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs_raw[];
+  XT* xs = reinterpret_cast<XT*>(xs_raw);  // (tokens, cols)
+  const int tid = threadIdx.x;
+  {
+    const int n16 = p.tokens * p.cols * (int)sizeof(XT) / 16;
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.x);
+    u32x4* dst = reinterpret_cast<u32x4*>(xs_raw);
+    for (int i = tid; i < n16; i += kPThreads) dst[i] = src[i];
+  }
+  __syncthreads();
   const int P = p.per_row;
-  const int part = gtid % P;
-  const int r = gtid / P;
+  const int part = tid % P;
+  const int r = blockIdx.x * (kPThreads / P) + tid / P;
   const bool live = r < p.rows;
   const int row = live ? r : p.rows - 1;  // lanes of a row past the end keep to the shuffles, write nothing
   const int blocks = p.cols / 256;
-  const XT* x = reinterpret_cast<const XT*>(p.x);
   float sum[kPMaxTokens];
 #pragma unroll
   for (int t = 0; t < kPMaxTokens; ++t) sum[t] = 0.0f;
   for (int h = part; h < 2 * blocks; h += P) {  // half a block, 128 weights, at a time
     const int64_t blk = (int64_t)row * blocks + h / 2;
     const int n = h % 2;
-    uint32_t hw[8], qw[8];
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      hw[w] = p.hm[blk * 8 + w];
-      qw[w] = p.qs[blk * 16 + 8 * n + w];
-    }
+    const u32x4* hm4 = reinterpret_cast<const u32x4*>(p.hm + blk * 8);
+    const u32x4* qs4 = reinterpret_cast<const u32x4*>(p.qs + blk * 16 + 8 * n);
+    const u32x4 h0 = hm4[0], h1 = hm4[1], q0 = qs4[0], q1 = qs4[1];
+    const uint32_t hw[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+    const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+    const u32x2 scw = *reinterpret_cast<const u32x2*>(p.sc + blk * 16 + 8 * n);  // the half's eight scales
     const float d = (float)p.dd[blk];
     const int base = (h / 2) * 256 + 128 * n;
 #pragma unroll
@@ -95,7 +106,7 @@ __global__ __launch_bounds__(kPThreads) void q3k_window_kernel(PlanesParams p) {
 #pragma unroll
         for (int t = 0; t < kPMaxTokens; ++t) {
           if (t < p.tokens) {
-            const XT* xt = x + (int64_t)t * p.cols + xi;
+            const XT* xt = xs + t * p.cols + xi;
             float dot = v[0] * to_f32(xt[0]);
             dot = __fmaf_rn(v[1], to_f32(xt[1]), dot);
             dot = __fmaf_rn(v[2], to_f32(xt[2]), dot);
@@ -107,7 +118,8 @@ __global__ __launch_bounds__(kPThreads) void q3k_window_kernel(PlanesParams p) {
           }
         }
       }
-      const float s0 = d * (float)p.sc[blk * 16 + 2 * rr], s1 = d * (float)p.sc[blk * 16 + 2 * rr + 1];
+      const uint32_t sw = scw[j / 2] >> (16 * (j % 2));  // scales 2 rr, 2 rr + 1 of the half
+      const float s0 = d * (float)(int8_t)(sw & 255u), s1 = d * (float)(int8_t)((sw >> 8) & 255u);
 #pragma unroll
       for (int t = 0; t < kPMaxTokens; ++t) sum[t] += __fmaf_rn(s0, acc0[t], s1 * acc1[t]);
     }
@@ -172,20 +184,20 @@ int strata_q3k_planes_window(const uint32_t* hm, const uint32_t* qs, const int8_
   if (tokens < 0) return STRATA_ERR_ARG;
   if (rows == 0 || tokens == 0) return STRATA_OK;
   if (!hm || !qs || !sc || !dd || !x || !out) return STRATA_ERR_ARG;
-  if (tokens > kPMaxTokens) return STRATA_ERR_SHAPE;
   if (per_row < 1 || per_row > 64 || (per_row & (per_row - 1))) return STRATA_ERR_ARG;
+  if (x_dtype != DT_F32 && x_dtype != DT_F16 && x_dtype != DT_BF16) return STRATA_ERR_DTYPE;
+  const size_t x_bytes = (size_t)tokens * (size_t)cols * (x_dtype == DT_F32 ? 4 : 2);
+  if (tokens > kPMaxTokens || x_bytes > kPMaxXBytes) return STRATA_ERR_SHAPE;
   PlanesParams p = {hm, qs, sc, (const f16*)dd, x, out, (int)rows, (int)cols, (int)tokens, per_row};
   const int64_t threads = rows * per_row;
   const dim3 grid((unsigned)((threads + kPThreads - 1) / kPThreads));
   hipStream_t s = (hipStream_t)stream;
   if (x_dtype == DT_F32)
-    hipLaunchKernelGGL(q3k_window_kernel<float>, grid, dim3(kPThreads), 0, s, p);
+    hipLaunchKernelGGL(q3k_window_kernel<float>, grid, dim3(kPThreads), x_bytes, s, p);
   else if (x_dtype == DT_F16)
-    hipLaunchKernelGGL(q3k_window_kernel<f16>, grid, dim3(kPThreads), 0, s, p);
-  else if (x_dtype == DT_BF16)
-    hipLaunchKernelGGL(q3k_window_kernel<bf16_t>, grid, dim3(kPThreads), 0, s, p);
+    hipLaunchKernelGGL(q3k_window_kernel<f16>, grid, dim3(kPThreads), x_bytes, s, p);
   else
-    return STRATA_ERR_DTYPE;
+    hipLaunchKernelGGL(q3k_window_kernel<bf16_t>, grid, dim3(kPThreads), x_bytes, s, p);
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }
