@@ -150,22 +150,22 @@ template <int KIND>
 struct TableFetch {
   uint32_t g[2] = {0, 0};
 };
-template <int KIND>
+template <int KIND, int NT = kThreads>  // NT threads to the workgroup
 __device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
   if constexpr (FastTraits<KIND>::grid > 0) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int i = min(tid + k * kThreads, FastTraits<KIND>::grid - 1);
+      const int i = min(tid + k * NT, FastTraits<KIND>::grid - 1);
       tf.g[k] = KIND == K_IQ3_S ? kStrataIq3sGrid[i] : kStrataIq3xxsGrid[i];
     }
   }
 }
-template <int KIND>
+template <int KIND, int NT = kThreads>
 __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableFetch<KIND>& tf, int tid) {
   if constexpr (FastTraits<KIND>::grid > 0) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int i = tid + k * kThreads;
+      const int i = tid + k * NT;
       const uint32_t g = tf.g[k];
       if (i < FastTraits<KIND>::grid)
         t.grid[i] = u32x2{pack_h2((float)(g & 255), (float)((g >> 8) & 255)),
@@ -177,7 +177,7 @@ __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableF
     t.sign4[tid] = u32x2{m[0], m[1]};
   }
   if constexpr (FastTraits<KIND>::q2 > 0) {
-    for (int i = tid; i < 256; i += kThreads)
+    for (int i = tid; i < 256; i += NT)
       t.q2[i] = u32x2{pack_h2((float)(i & 3) - 1.0f, (float)((i >> 2) & 3) - 1.0f),
                       pack_h2((float)((i >> 4) & 3) - 1.0f, (float)(i >> 6) - 1.0f)};
   }
