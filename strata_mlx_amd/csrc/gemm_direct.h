@@ -24,7 +24,6 @@ constexpr int kDStep = 256;                  // columns a K step
 constexpr int kDPitch = kDStep + 8;          // LDS pitch of a slot's activations (float16), against bank conflicts
 constexpr int kDTiles = 4;                   // tiles a group
 constexpr int kDRuns = kDStep / 32;          // runs of a row a step: one MFMA each
-constexpr int kDRing = 2;                    // K steps of fields held: the one decoded and one loading
 
 // What lane slice g of one row holds of a K step: each run's two index (code) bytes for groups 2g and 2g + 1,
 // and the fields the run's groups share.
@@ -50,47 +49,51 @@ struct StepSlice<K_Q2_0> {
   uint32_t d[kDRuns / 2];  // a block's d (two runs a block)
 };
 
+// A K step of a row as the kernel stages it: the step's bytes (one IQ3 block, four Q2_0 blocks) in 16-byte chunks,
+// the last one ending at the step's end.
 template <int KIND>
-__device__ __forceinline__ void load_slice(const uint8_t* row, int k, int g, StepSlice<KIND>& f) {
-  using strata_mv::load_unaligned;
-  if constexpr (KIND == K_IQ3_S) {  // d @0, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106
-    const uint8_t* b = row + k * 110;
-    f.d = load_unaligned<uint16_t>(b);
-#pragma unroll
-    for (int q = 0; q < kDRuns; ++q) f.qs[q] = load_unaligned<uint16_t>(b + 2 + 8 * q + 2 * g);
-    f.qh = load_unaligned<u32x2>(b + 66);
-    f.sg[0] = load_unaligned<u32x4>(b + 74);
-    f.sg[1] = load_unaligned<u32x4>(b + 90);
-    f.sc = load_unaligned<uint32_t>(b + 106);
-  } else if constexpr (KIND == K_IQ3_XXS) {  // d @0, qs[64] @2, aux[8] (u32) @66
-    const uint8_t* b = row + k * 98;
-    f.d = load_unaligned<uint16_t>(b);
-#pragma unroll
-    for (int q = 0; q < kDRuns; ++q) f.qs[q] = load_unaligned<uint16_t>(b + 2 + 8 * q + 2 * g);
-    f.aux[0] = load_unaligned<u32x4>(b + 66);
-    f.aux[1] = load_unaligned<u32x4>(b + 82);
-  } else {  // Q2_0, four blocks of 18 bytes (d @0, qs[16] @2); run q: block q / 2, code bytes 8 (q % 2) on
-    const uint8_t* b = row + k * 72;
-#pragma unroll
-    for (int j = 0; j < kDRuns / 2; ++j) f.d[j] = load_unaligned<uint16_t>(b + 18 * j);
-#pragma unroll
-    for (int q = 0; q < kDRuns; ++q) f.qs[q] = load_unaligned<uint16_t>(b + 18 * (q / 2) + 2 + 8 * (q % 2) + 2 * g);
-  }
+struct StepBytes {
+  static constexpr int bytes = KIND == K_IQ3_S ? 110 : KIND == K_IQ3_XXS ? 98 : 72;
+  static constexpr int chunks = (bytes + 15) / 16;
+  static constexpr int pitch = 16 * chunks;  // a row's bytes in the slab (28 or 20 dwords: the 16 rows' fields
+                                             // fall in different banks)
+  __device__ static int offset(int c) { return min(16 * c, bytes - 16); }
+};
+
+template <typename T>
+__device__ __forceinline__ T lds_load(const uint8_t* p) {
+  typedef const __attribute__((address_space(3))) strata_mv::Unaligned<T> L;
+  return ((L*)(const __attribute__((address_space(3))) uint8_t*)p)->v;
+}
+template <typename T>
+__device__ __forceinline__ void lds_store(uint8_t* p, T v) {
+  typedef __attribute__((address_space(3))) strata_mv::Unaligned<T> L;
+  ((L*)(__attribute__((address_space(3))) uint8_t*)p)->v = v;
 }
 
-// The compiler no longer knows the fields' values: their decode cannot move above this point (nor its waits
-// for the loads).
+// Lane slice g of a step's bytes b (in LDS): each run's two index (code) bytes of groups 2g and 2g + 1, and the
+// run's shared fields.
 template <int KIND>
-__device__ __forceinline__ void opaque_slice(StepSlice<KIND>& f) {
+__device__ __forceinline__ void read_slice(const uint8_t* b, int g, StepSlice<KIND>& f) {
+  if constexpr (KIND == K_IQ3_S) {  // d @0, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106
+    f.d = lds_load<uint16_t>(b);
 #pragma unroll
-  for (int q = 0; q < kDRuns; ++q) asm volatile("" : "+v"(f.qs[q]));
-  if constexpr (KIND == K_IQ3_S) {
-    asm volatile("" : "+v"(f.qh), "+v"(f.sg[0]), "+v"(f.sg[1]), "+v"(f.sc), "+v"(f.d));
-  } else if constexpr (KIND == K_IQ3_XXS) {
-    asm volatile("" : "+v"(f.aux[0]), "+v"(f.aux[1]), "+v"(f.d));
-  } else {
+    for (int q = 0; q < kDRuns; ++q) f.qs[q] = lds_load<uint16_t>(b + 2 + 8 * q + 2 * g);
+    f.qh = lds_load<u32x2>(b + 66);
+    f.sg[0] = lds_load<u32x4>(b + 74);
+    f.sg[1] = lds_load<u32x4>(b + 90);
+    f.sc = lds_load<uint32_t>(b + 106);
+  } else if constexpr (KIND == K_IQ3_XXS) {  // d @0, qs[64] @2, aux[8] (u32) @66
+    f.d = lds_load<uint16_t>(b);
 #pragma unroll
-    for (int j = 0; j < kDRuns / 2; ++j) asm volatile("" : "+v"(f.d[j]));
+    for (int q = 0; q < kDRuns; ++q) f.qs[q] = lds_load<uint16_t>(b + 2 + 8 * q + 2 * g);
+    f.aux[0] = lds_load<u32x4>(b + 66);
+    f.aux[1] = lds_load<u32x4>(b + 82);
+  } else {  // Q2_0, four blocks of 18 bytes (d @0, qs[16] @2); run q: block q / 2, code bytes 8 (q % 2) on
+#pragma unroll
+    for (int j = 0; j < kDRuns / 2; ++j) f.d[j] = lds_load<uint16_t>(b + 18 * j);
+#pragma unroll
+    for (int q = 0; q < kDRuns; ++q) f.qs[q] = lds_load<uint16_t>(b + 18 * (q / 2) + 2 + 8 * (q % 2) + 2 * g);
   }
 }
 
@@ -133,47 +136,69 @@ __device__ __forceinline__ float decode_slice(const StepSlice<KIND>& f, int q, i
 }
 
 // This thread's share of K step k's activations of the group (16-byte chunks of 16 slots x 256 columns a tile:
-// one a thread a tile), as float16.
+// one a thread a tile), as they are in memory: they are converted when they go to LDS, a step later, so that
+// nothing waits for them before then.
 template <typename AT>
 __device__ __forceinline__ void load_step_acts(const AT* a, const GemmParams& p, int t0, int nt, int k, int tid,
                                                u32x4 (&av)[kDTiles]) {
   static_assert(kGThreads == 16 * (kDStep / 8), "one 16-byte chunk of a tile's step a thread");
   const int slot = tid / (kDStep / 8), col = (tid % (kDStep / 8)) * 8;
 #pragma unroll
+  for (int i = 0; i < kDTiles; ++i)
+    if (i < nt) av[i] = *reinterpret_cast<const u32x4*>(a + ((int64_t)(t0 + i) * 16 + slot) * p.cols + k * kDStep + col);
+}
+
+// The chunks to LDS as float16 (bfloat16 converted: exact in float16's range).
+template <typename AT>
+__device__ __forceinline__ void store_step_acts(f16* a_lds, int nt, int tid, const u32x4 (&av)[kDTiles]) {
+#pragma unroll
   for (int i = 0; i < kDTiles; ++i) {
     if (i < nt) {
-      const AT* src = a + ((int64_t)(t0 + i) * 16 + slot) * p.cols + k * kDStep + col;
-      if constexpr (std::is_same<AT, f16>::value) {
-        av[i] = *reinterpret_cast<const u32x4*>(src);
-      } else {
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(src);  // 8 bfloat16
-        u32x4 o;
+      u32x4 o = av[i];
+      if constexpr (!std::is_same<AT, f16>::value) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float lo = __uint_as_float(raw[q] << 16), hi = __uint_as_float(raw[q] & 0xffff0000u);
+          const float lo = __uint_as_float(av[i][q] << 16), hi = __uint_as_float(av[i][q] & 0xffff0000u);
           o[q] = (uint32_t)__builtin_bit_cast(uint16_t, (f16)lo) |
                  ((uint32_t)__builtin_bit_cast(uint16_t, (f16)hi) << 16);
         }
-        av[i] = o;
       }
+      *reinterpret_cast<u32x4*>(a_lds + (i * 16 + tid / 32) * kDPitch + (tid % 32) * 8) = o;
     }
   }
 }
 
-// The K loop of a group of NT tiles (a template parameter: the loop is straight-line code, which the compiler
-// interleaves: decode of one run with the MFMAs and sums of the last). Fields of step k + kDRing - 1 are loaded
-// while step k is decoded; the activations of step k + 1 while step k is multiplied.
+// The K loop of a group of up to NT tiles (nt of them). A wave stages its 16 rows' bytes of a step in its own LDS
+// slab: two 16-byte loads a lane (chunk L of the 16 rows' chunks: row L / chunks), loaded a step ahead, written to
+// the slab when the step comes, then read back as the lanes' slices. One wave writes and reads its slab, so no
+// barrier guards it (a wave's LDS operations are done in order). The activations of step k + 1 are loaded while
+// step k is multiplied.
 template <int KIND, typename AT, int NT>
 __device__ __forceinline__ void group_product(const GemmParams& p, const strata_mv::DirectTables<KIND>& tab,
-                                              f16* a_lds, const uint8_t* wrow, int t0, int row, int tid, int nt) {
+                                              f16* a_lds, uint8_t* slab, const uint8_t* mat, int n0w, int t0,
+                                              int row, int tid, int nt) {
+  using SB = StepBytes<KIND>;
   const int lane = tid % 64, n = lane % 16, g = lane / 16;
   const AT* a = reinterpret_cast<const AT*>(p.a);
   const int nsteps = p.cols / kDStep;
 
-  StepSlice<KIND> f[kDRing];
+  // the lane's two chunks: rows and offsets (lanes past the 16 rows' chunks load the last again, write nothing)
+  constexpr int kChunks = 16 * SB::chunks;
+  static_assert(kChunks <= 128, "two chunks a lane");
+  const uint8_t* src[2];
+  int dst[2];
+  bool put[2];
 #pragma unroll
-  for (int s = 0; s < kDRing - 1; ++s)
-    if (s < nsteps) load_slice<KIND>(wrow, s, g, f[s]);
+  for (int h = 0; h < 2; ++h) {
+    const int L = min(lane + 64 * h, kChunks - 1);
+    const int r = L / SB::chunks, c = L % SB::chunks;
+    src[h] = mat + (int64_t)min(n0w + r, p.rows - 1) * p.row_bytes + SB::offset(c);
+    dst[h] = r * SB::pitch + SB::offset(c);
+    put[h] = lane + 64 * h < kChunks;
+  }
+  u32x4 raw[2][2];  // the ring: step k's chunks, step k + 1's in flight
+#pragma unroll
+  for (int h = 0; h < 2; ++h) raw[0][h] = strata_mv::load_unaligned<u32x4>(src[h]);
   u32x4 av[kDTiles];
   load_step_acts<AT>(a, p, t0, nt, 0, tid, av);
 
@@ -181,24 +206,29 @@ __device__ __forceinline__ void group_product(const GemmParams& p, const strata_
 #pragma unroll
   for (int i = 0; i < NT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = 0; kb < nsteps; kb += kDRing) {
+  for (int kb = 0; kb < nsteps; kb += 2) {
 #pragma unroll
-    for (int s = 0; s < kDRing; ++s) {
+    for (int s = 0; s < 2; ++s) {
       const int k = kb + s;
       if (k < nsteps) {
-        // fields of step k + kDRing - 1 go to the ring slot step k - 1 used
-        if (k + kDRing - 1 < nsteps) load_slice<KIND>(wrow, k + kDRing - 1, g, f[(s + kDRing - 1) % kDRing]);
-        __syncthreads();  // every wave's reads of the last step's activations are done (and the tables written)
+        // step k + 1's chunks (past the last step the last again: unconditional loads, which the waits for
+        // earlier loads can count on)
+        const int64_t next = (int64_t)min(k + 1, nsteps - 1) * SB::bytes;
 #pragma unroll
-        for (int i = 0; i < NT; ++i)
-          if (i < nt) *reinterpret_cast<u32x4*>(a_lds + (i * 16 + tid / 32) * kDPitch + (tid % 32) * 8) = av[i];
+        for (int h = 0; h < 2; ++h) raw[(s + 1) % 2][h] = strata_mv::load_unaligned<u32x4>(src[h] + next);
+        __syncthreads();  // every wave's reads of the last step's activations are done (and the tables written)
+        store_step_acts<AT>(a_lds, nt, tid, av);
         if (k + 1 < nsteps) load_step_acts<AT>(a, p, t0, nt, k + 1, tid, av);
-        opaque_slice<KIND>(f[s]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (put[h]) lds_store<u32x4>(slab + dst[h], raw[s][h]);
+        StepSlice<KIND> f;
+        read_slice<KIND>(slab + n * SB::pitch, g, f);
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < kDRuns; ++q) {
           uint32_t w[4];
-          const float sc = decode_slice<KIND>(f[s], q, g, w, tab);
+          const float sc = decode_slice<KIND>(f, q, g, w, tab);
           const f16x8 bv = __builtin_bit_cast(f16x8, u32x4{w[0], w[1], w[2], w[3]});
 #pragma unroll
           for (int i = 0; i < NT; ++i) {
@@ -229,6 +259,7 @@ template <int KIND, typename AT>
 __global__ __launch_bounds__(kGThreads, 4) void direct_gemm_kernel(GemmParams p) {
   __shared__ strata_mv::DirectTables<KIND> tab;
   __shared__ __attribute__((aligned(16))) f16 a_lds[kDTiles * 16 * kDPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t slabs[kGWaves * 16 * StepBytes<KIND>::pitch];
 
   const int tid = threadIdx.x, lane = tid % 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -248,15 +279,15 @@ __global__ __launch_bounds__(kGThreads, 4) void direct_gemm_kernel(GemmParams p)
 
   // lane (n, g): row n of the wave's 16, columns 8g .. 8g + 7 of each run
   const int row = n0 + wave * 16 + lane % 16;
-  const uint8_t* wrow = p.blocks + (int64_t)e * p.mat_bytes + (int64_t)min(row, p.rows - 1) * p.row_bytes;
+  const uint8_t* mat = p.blocks + (int64_t)e * p.mat_bytes;
   {
     strata_mv::TableFetch<KIND> tf;
     strata_mv::fetch_tables<KIND, kGThreads>(tf, tid);
     strata_mv::store_tables<KIND, kGThreads>(tab, tf, tid);  // read after the K loop's first barrier
   }
-  static_assert(kDTiles == 4, "one K loop for each group size");
   nt = __builtin_amdgcn_readfirstlane(nt);
-  group_product<KIND, AT, 4>(p, tab, a_lds, wrow, t0, row, tid, nt);
+  group_product<KIND, AT, kDTiles>(p, tab, a_lds, slabs + wave * 16 * StepBytes<KIND>::pitch, mat, n0 + wave * 16,
+                                    t0, row, tid, nt);
 }
 
 template <int KIND>
