@@ -2,15 +2,17 @@
 //
 // c[s, :] = W[e(s)] . a[s, :] over tiles of 16 slots, each tile one expert's (strata_mlx/blocks.py:583-654).
 // A workgroup (kGWaves waves) takes 16 output rows a wave of one expert and its tiles within an aligned window of
-// four tiles; it is the workgroup at the group's first tile that works, the others of the column exit at once.
+// kDTiles tiles; it is the workgroup at the group's first tile that works, the others of the column exit at once.
 // A K step is 256 columns (one IQ3 block, four Q2_0 blocks, of every row), eight runs of 32, one MFMA each:
 // v_mfma_f32_16x16x32_f16, a (16 slots x 32) x w (32 x 16 rows). Lane (n, g) of a wave gives the MFMA row n's
-// columns 8g .. 8g + 7 of the run, which are groups 2g and 2g + 1 of the run: it loads exactly their fields (the
-// two index or code bytes, and the run's shared sign, scale and high-bit fields) and decodes them in registers
-// into exact float16 integers (codebook entry with its sign). The product times the row's run scale is added to
-// the float32 sums, so nothing is rounded. The weights never pass through LDS; the group's activations for a
-// step do (bfloat16 converted to float16 as they load), shared by the workgroup's waves. An expert's weights
-// are read and decoded once per window of four tiles it has tiles in.
+// columns 8g .. 8g + 7 of the run, which are groups 2g and 2g + 1 of the run. A wave stages its 16 rows' bytes
+// of the step in its own LDS slab (coalesced 16-byte loads, a step ahead); each lane reads back exactly its
+// fields (the two index or code bytes, and the run's shared sign, scale and high-bit fields) and decodes them in
+// registers into exact float16 integers (codebook entry with its sign). The product times the row's run scale
+// is added to the float32 sums, so nothing is rounded. The group's activations for a step go to LDS (bfloat16
+// converted to float16 on the way), shared by the workgroup's waves. An expert's weights are read and decoded
+// once per window of kDTiles tiles it has tiles in: two tiles a window keeps the kernel under 90 VGPRs (five or
+// six waves a SIMD), which is worth more than decoding the weights of experts with three or more tiles again.
 #pragma once
 #include "direct_impl.h"
 #include "gemm_impl.h"
@@ -22,7 +24,7 @@ constexpr int kGThreads = 64 * kGWaves;
 constexpr int kDRows = 16 * kGWaves;         // output rows a workgroup
 constexpr int kDStep = 256;                  // columns a K step
 constexpr int kDPitch = kDStep + 8;          // LDS pitch of a slot's activations (float16), against bank conflicts
-constexpr int kDTiles = 4;                   // tiles a group
+constexpr int kDTiles = 2;                   // tiles a group
 constexpr int kDRuns = kDStep / 32;          // runs of a row a step: one MFMA each
 
 // What lane slice g of one row holds of a K step: each run's two index (code) bytes for groups 2g and 2g + 1,
