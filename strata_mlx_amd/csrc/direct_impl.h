@@ -1,4 +1,5 @@
-// The decode matvec for float16 activations, rows read straight into registers (IQ3_S, IQ3_XXS, Q2_0).
+// The decode matvec for float16 activations, rows read straight into registers (IQ3_S, IQ3_XXS, Q2_0 with
+// their codebooks in LDS; Q4_K, Q6_K, Q8_0 decoded by byte arithmetic alone).
 //
 // A decode call moves tens of megabytes in a few microseconds, so what matters is that every byte is requested
 // at once: a wave's loads go out as soon as it knows its expert, before anything else it does. Nothing is staged
@@ -48,6 +49,33 @@ struct RunPair<K_Q2_0> {
   u32x4 qs;     // the block's 16 code bytes
   uint32_t d;
 };
+// The kinds decoded without a codebook: a lane's 64 weights are two Q8_0 blocks, a quarter of a Q4_K block (the
+// low and high nibbles of 32 bytes), or two runs of a Q6_K half block (r0 and r0 + 2: the low and high nibbles of
+// 32 ql bytes, bits 2r .. 2r + 1 of the half's 32 qh bytes).
+template <>
+struct RunPair<K_Q8_0> {
+  u32x4 q[4];   // the two blocks' 32 int8 codes each
+  uint32_t d[2];
+};
+template <>
+struct RunPair<K_Q4_K> {
+  u32x4 qs[2];  // 32 bytes: the first run's codes in the low nibbles, the second's in the high
+  u32x4 sm;     // the 12 packed scale / min bytes (and 4 bytes past them)
+  uint32_t dd;  // d | dmin << 16
+};
+template <>
+struct RunPair<K_Q6_K> {
+  u32x4 ql[2];     // 32 bytes: run r0's low four bits in the low nibbles, run r0 + 2's in the high
+  u32x4 qh[2];     // the half's 32 high-bit bytes
+  uint32_t sc[2];  // each run's two int8 scales (16 weights a scale)
+  uint32_t d;
+};
+
+template <int KIND>
+struct DirectKind {
+  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K;
+  static constexpr bool any = FastTraits<KIND>::supported || linear;
+};
 
 // A load from global memory at any alignment (gfx950 serves 2-byte aligned dwordx2/x4 loads as they are).
 template <typename T>
@@ -79,6 +107,8 @@ __device__ __forceinline__ void load_pair(const uint8_t* row, int j, RunPair<KIN
     f.d = load_unaligned<uint16_t>(b);
     f.qs = load_unaligned<u32x4>(b + 2 + 8 * ib0);
     f.aux = load_unaligned<u32x2>(b + 66 + 4 * ib0);
+  } else if constexpr (DirectKind<KIND>::linear) {
+    static_assert(KIND != KIND, "the linear kinds load through load_fields");
   } else {  // Q2_0: d @0, qs[16] @2
     const uint8_t* b = row + j * 18;
     f.d = load_unaligned<uint16_t>(b);
@@ -144,6 +174,82 @@ __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint
   }
 }
 
+// Four code bytes -> two words of float16 integers, each code less `bias`: 0x64nn is 1024 + nn, and 1024 + bias
+// is subtracted from both halves at once (exact: integers below 2048).
+template <int BIAS>
+__device__ __forceinline__ void bytes_to_h2(uint32_t b, uint32_t* w2) {
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  const h2v k = h2v{(_Float16)(1024.0f + BIAS), (_Float16)(1024.0f + BIAS)};
+  w2[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) - k);
+  w2[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) - k);
+}
+
+// A run's scales: a (every kind), b (Q4_K: dmin * min, subtracted times the run's sum of x; Q6_K: the second
+// 16 weights' scale, a the first 16's).
+struct RunScale {
+  float a, b;
+};
+
+// Run h (0, 1) of lane run pair j: 16 packed float16 pairs of integers into w, and its scales.
+template <int KIND>
+__device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, int j, uint32_t* w,
+                                               const DirectTables<KIND>& t) {
+  if constexpr (KIND == K_Q8_0) {  // w = d * q, strata_mlx/gguf.py:203-206
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bytes_to_h2<128>(f.q[2 * h + i / 4][i % 4] ^ 0x80808080u, w + 2 * i);
+    return RunScale{half_bits(f.d[h]), 0.0f};
+  } else if constexpr (KIND == K_Q4_K) {  // w = code * (d * sc) - dmin * mn, strata_mlx/gguf.py:174-179, 207-217
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bytes_to_h2<0>((f.qs[i / 4][i % 4] >> (4 * h)) & 0x0F0F0F0Fu, w + 2 * i);
+    // sub-block s = 2 (j % 4) + h of the block: its 6-bit scale and min from the 12 packed bytes p
+    const int sb = 2 * (j & 3) + h, tb = 8 * (sb & 3);
+    const uint32_t b0 = (f.sm[0] >> tb) & 255, b1 = (f.sm[1] >> tb) & 255, b2 = (f.sm[2] >> tb) & 255;
+    const bool hi = sb >= 4;
+    const uint32_t sc = hi ? ((b2 & 15) | ((b0 >> 6) << 4)) : (b0 & 63);
+    const uint32_t mn = hi ? ((b2 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63);
+    return RunScale{half_bits(f.dd & 0xffff) * (float)sc, half_bits(f.dd >> 16) * (float)mn};
+  } else if constexpr (KIND == K_Q6_K) {  // w = (code - 32) * scale * d, strata_mlx/gguf.py:150-165
+    const int r2 = 2 * ((j & 1) + 2 * h);  // the run's bits in the high-bit bytes
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t lo = (f.ql[i / 4][i % 4] >> (4 * h)) & 0x0F0F0F0Fu;
+      const uint32_t hb = (f.qh[i / 4][i % 4] >> r2) & 0x03030303u;
+      bytes_to_h2<32>(lo | (hb << 4), w + 2 * i);
+    }
+    const float d = half_bits(f.d);
+    return RunScale{d * (float)(int8_t)(f.sc[h] & 255), d * (float)(int8_t)(f.sc[h] >> 8)};
+  } else {
+    return RunScale{decode_pair<KIND>(f, h, w, t), 0.0f};
+  }
+}
+
+// Sum of 2n packed float16 products, in two float32 chains (as dot16x2 adds them).
+template <int N>
+__device__ __forceinline__ float dot_n(const uint32_t* w, const uint32_t* x) {
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; i += 2) {
+    a = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, w[i]), __builtin_bit_cast(h2_t, x[i]), a, false);
+    b = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, w[i + 1]), __builtin_bit_cast(h2_t, x[i + 1]), b, false);
+  }
+  return a + b;
+}
+
+// The run's sum against 32 activations (16 packed pairs).
+template <int KIND>
+__device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w, const uint32_t* x) {
+  if constexpr (KIND == K_Q4_K) {
+    const uint32_t ones[16] = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                               0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                               0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+    return s.a * dot16x2(w, x) - s.b * dot_n<16>(ones, x);
+  } else if constexpr (KIND == K_Q6_K) {
+    return s.a * dot_n<8>(w, x) + s.b * dot_n<8>(w + 8, x + 8);
+  } else {
+    return s.a * dot16x2(w, x);
+  }
+}
+
 // The codebook tables in two halves: the constants' loads go out before the rows' (a wait for them is then not
 // a wait for the rows), the LDS entries are written after.
 template <int KIND>
@@ -186,9 +292,23 @@ __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableF
 // The compiler no longer knows the fields' values: code that decodes them cannot move above this point.
 template <int KIND>
 __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
+  if constexpr (KIND == K_Q8_0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(f.q[i]));
+    asm volatile("" : "+v"(f.d[0]), "+v"(f.d[1]));
+    return;
+  } else if constexpr (KIND == K_Q4_K) {
+    asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.sm), "+v"(f.dd));
+    return;
+  } else if constexpr (KIND == K_Q6_K) {
+    asm volatile("" : "+v"(f.ql[0]), "+v"(f.ql[1]), "+v"(f.qh[0]), "+v"(f.qh[1]), "+v"(f.sc[0]), "+v"(f.sc[1]),
+                 "+v"(f.d));
+    return;
+  } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(f.qs[i]));
   asm volatile("" : "+v"(f.d));
+  }
   if constexpr (KIND == K_IQ3_S) {
     asm volatile("" : "+v"(f.qh), "+v"(f.sc), "+v"(f.sg[0]), "+v"(f.sg[1]));
   } else if constexpr (KIND == K_IQ3_XXS) {
@@ -230,11 +350,33 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.d = b;
     o.qs = b + 2 + 16 * jj;
     o.a = b + 66 + 8 * jj;
+  } else if constexpr (KIND == K_Q8_0) {  // two blocks of 34: d @0, int8 q[32] @2
+    o.d = j * 68;
+    o.qs = j * 68 + 2;
+  } else if constexpr (KIND == K_Q4_K) {  // d, dmin @0, scales[12] @4, qs[128] @16 (sub-blocks 2k, 2k + 1 @16 + 32k)
+    const uint32_t b = (j >> 2) * 144, jj = j & 3;
+    o.d = b;
+    o.qs = b + 16 + 32 * jj;
+    o.a = b + 4;
+  } else if constexpr (KIND == K_Q6_K) {  // ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208
+    const uint32_t b = (j >> 2) * 210, hh = (j >> 1) & 1, r0 = j & 1;
+    o.d = b + 208;
+    o.qs = b + 64 * hh + 32 * r0;
+    o.a = b + 128 + 32 * hh;
+    o.b = b + 192 + 8 * hh + 2 * r0;  // run r0's two scales; run r0 + 2's four bytes on
   } else {  // Q2_0: d @0, qs[16] @2
     o.d = j * 18;
     o.qs = j * 18 + 2;
   }
   return o;
+}
+
+// The row's run (32 weights) that half h of lane run pair j multiplies: 2j + h, except Q6_K, whose lane takes
+// runs r0 and r0 + 2 of a half block (block j / 4, half (j / 2) % 2, r0 = j % 2).
+template <int KIND>
+__device__ __forceinline__ int run_of(int j, int h) {
+  if constexpr (KIND == K_Q6_K) return 8 * (j >> 2) + 4 * ((j >> 1) & 1) + (j & 1) + 2 * h;
+  return 2 * j + h;
 }
 
 // A load at base + off: base the same for the whole wave, off the lane's (global_load v, v_off, s_base).
@@ -248,6 +390,30 @@ __device__ __forceinline__ T load_at(const uint8_t* base, uint32_t off) {
 template <int KIND>
 __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, const LaneOffsets<KIND>& o,
                                             RunPair<KIND>& f) {
+  if constexpr (KIND == K_Q8_0) {
+    f.d[0] = load_at<uint16_t>(row, lo + o.d);
+    f.q[0] = load_at<u32x4>(row, lo + o.qs);
+    f.q[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    f.d[1] = load_at<uint16_t>(row, lo + o.d + 34);
+    f.q[2] = load_at<u32x4>(row, lo + o.qs + 34);
+    f.q[3] = load_at<u32x4>(row, lo + o.qs + 50);
+    return;
+  } else if constexpr (KIND == K_Q4_K) {
+    f.dd = load_at<uint32_t>(row, lo + o.d);
+    f.sm = load_at<u32x4>(row, lo + o.a);
+    f.qs[0] = load_at<u32x4>(row, lo + o.qs);
+    f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    return;
+  } else if constexpr (KIND == K_Q6_K) {
+    f.d = load_at<uint16_t>(row, lo + o.d);
+    f.sc[0] = load_at<uint16_t>(row, lo + o.b);
+    f.sc[1] = load_at<uint16_t>(row, lo + o.b + 4);
+    f.ql[0] = load_at<u32x4>(row, lo + o.qs);
+    f.ql[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    f.qh[0] = load_at<u32x4>(row, lo + o.a);
+    f.qh[1] = load_at<u32x4>(row, lo + o.a + 16);
+    return;
+  } else {
   f.d = load_at<uint16_t>(row, lo + o.d);
   f.qs = load_at<u32x4>(row, lo + o.qs);
   if constexpr (KIND == K_IQ3_S) {
@@ -256,6 +422,7 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
     f.sc = load_at<uint8_t>(row, lo + o.c);
   } else if constexpr (KIND == K_IQ3_XXS) {
     f.aux = load_at<u32x2>(row, lo + o.a);
+  }
   }
 }
 
@@ -353,8 +520,8 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
 #pragma unroll
     for (int k = 0; k < 2; ++k) xv[k] = src[min(tid + k * kThreads, p.cols / 8 - 1)];
   } else if constexpr (!GLU) {
-    fast_load_x<false>(p, q0, 2 * jp, x[0]);
-    fast_load_x<false>(p, q0, 2 * jp + 1, x[0] + 16);
+    fast_load_x<false>(p, q0, run_of<KIND>(jp, 0), x[0]);
+    fast_load_x<false>(p, q0, run_of<KIND>(jp, 1), x[0] + 16);
   }
   const LaneOffsets<KIND> lo = lane_offsets<KIND>(jp);
   RunPair<KIND> f[RU];
@@ -362,12 +529,19 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   for (int s = 0; s < RU; ++s) {
     const int rb = r0 + (PAIRED ? s / 2 : s) * side;  // the step's first row, the same for the whole wave
     const int rw = min(rb, p.rows - 1), rl = min(rb + sub, p.rows - 1);
+    if constexpr (DirectKind<KIND>::linear && !PAIRED) {
+      if (p.row_ids != nullptr) {  // listed rows (dense): an id past the matrix reads row 0 and writes NaN
+        const uint32_t id = p.row_ids[rl];
+        load_fields<KIND>(m0, (id < (uint32_t)p.src_rows ? id : 0u) * (uint32_t)p.row_bytes, lo, f[s]);
+        continue;
+      }
+    }
     const uint8_t* row = (PAIRED && (s & 1) ? m1 : m0) + (int64_t)rw * p.row_bytes;
     load_fields<KIND>(row, (uint32_t)(rl - rw) * p.row_bytes, lo, f[s]);
   }
   if constexpr (GLU) {  // silu(gate) * up waits for its loads: after the rows' have gone out
-    fast_load_x<true>(p, q0, 2 * jp, x[0]);
-    fast_load_x<true>(p, q0, 2 * jp + 1, x[0] + 16);
+    fast_load_x<true>(p, q0, run_of<KIND>(jp, 0), x[0]);
+    fast_load_x<true>(p, q0, run_of<KIND>(jp, 1), x[0] + 16);
   }
   // nothing above moves below this point, nothing below moves above it
   asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(tf.g[0]), "+v"(tf.g[1])::"memory");
@@ -401,7 +575,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   if (shared_x) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const u32x4 c = xs[8 * jp + v];
+      const u32x4 c = xs[4 * run_of<KIND>(jp, v / 4) + v % 4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[0][4 * v + i] = c[i];
     }
@@ -446,8 +620,8 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       if (t < nq && (pass > 0 || t > 0)) {
-        fast_load_x<GLU>(p, q[t], 2 * jp, x[t]);
-        fast_load_x<GLU>(p, q[t], 2 * jp + 1, x[t] + 16);
+        fast_load_x<GLU>(p, q[t], run_of<KIND>(jp, 0), x[t]);
+        fast_load_x<GLU>(p, q[t], run_of<KIND>(jp, 1), x[t] + 16);
       }
     }
     float acc[TT][RU];
@@ -460,10 +634,10 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         uint32_t w[16];
-        const float scale = decode_pair<KIND>(f[s], h, w, tab);
+        const RunScale rs = decode_run<KIND>(f[s], h, jp, w, tab);
 #pragma unroll
         for (int t = 0; t < TT; ++t)
-          if (t < nq) acc[t][s] += scale * dot16x2(w, x[t] + 16 * h);
+          if (t < nq) acc[t][s] += apply_run<KIND>(rs, w, x[t] + 16 * h);
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
@@ -503,7 +677,10 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
               if (p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = uq;
               reinterpret_cast<f16*>(p.glu_out)[o] = from_f32<f16>(h);
             } else {
-              reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(v);
+              float vo = v;
+              if constexpr (DirectKind<KIND>::linear)
+                if (p.row_ids != nullptr && p.row_ids[r] >= (uint32_t)p.src_rows) vo = __builtin_nanf("");
+              reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(vo);
             }
           }
         }
@@ -528,7 +705,10 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
                 if (p.out[1] != nullptr) reinterpret_cast<f16*>(p.out[1])[o] = uu;
                 reinterpret_cast<f16*>(p.glu_out)[o] = from_f32<f16>(swiglu_rounded<f16>(gg, uu));
               } else {
-                reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(sums[kk][t]);
+                float vo = sums[kk][t];
+                if constexpr (DirectKind<KIND>::linear)
+                  if (p.row_ids != nullptr && p.row_ids[r] >= (uint32_t)p.src_rows) vo = __builtin_nanf("");
+                reinterpret_cast<f16*>(p.out[z0])[o] = from_f32<f16>(vo);
               }
             }
           }
@@ -579,8 +759,12 @@ template <int KIND, bool GLU, bool PAIRED, int TT>
 int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
   // Q2_0 at two tokens a pass spills at four row steps (the compiler keeps more of its light decode in flight);
   // two steps give the same sums (each step's lanes meet by the same exchange)
-  if (row_steps() == 2 || (KIND == K_Q2_0 && TT > 1)) return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
-  return launch_direct_lt<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
+  if constexpr (DirectKind<KIND>::linear) {  // their wider fields spill at four row steps
+    return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
+  } else {
+    if (row_steps() == 2 || (KIND == K_Q2_0 && TT > 1)) return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
+    return launch_direct_lt<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
+  }
 }
 
 // Rows of 64 to 4096 weights in run pairs (every IQ3_S / IQ3_XXS / Q2_0 row), up to 256 pairs.
@@ -595,14 +779,33 @@ int launch_direct(MatvecParams& p, bool one_token, int grid_y, int grid_z, hipSt
   int L = 1;
   while (L < p.runs / 2) L *= 2;
   p.ct = L;
-  if (one_token) return launch_direct_tt<KIND, GLU, PAIRED, 1>(p, grid_y, grid_z, s);
-  return launch_direct_tt<KIND, GLU, PAIRED, 2>(p, grid_y, grid_z, s);
+  // the linear kinds take one token a pass (two spill), decoding their rows again for each token
+  if (one_token || DirectKind<KIND>::linear) return launch_direct_tt<KIND, GLU, PAIRED, 1>(p, grid_y, grid_z, s);
+  if constexpr (!DirectKind<KIND>::linear) return launch_direct_tt<KIND, GLU, PAIRED, 2>(p, grid_y, grid_z, s);
+  return STRATA_ERR_SHAPE;
 }
 
 // The float16 fast paths where they apply (a type of FastTraits, float16 in and out, rows contiguous): the
 // direct kernel, else the persistent wave kernel, else the staged fast kernel; other cases the generic kernels.
 template <int KIND>
 int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int grid_y, int grid_z, hipStream_t s) {
+  if constexpr (DirectKind<KIND>::linear) {  // float16 in and out, rows of run pairs: the direct kernel
+    // listed rows too (dense), when the matrix's byte offsets fit 32 bits: a listed row gets the bits of its
+    // layer's full product
+    const bool ids_ok = p.row_ids == nullptr ||
+                        (p.mode == MODE_DENSE && (int64_t)p.src_rows * p.row_bytes < ((int64_t)1 << 32));
+    if (x_dtype == DT_F16 && out_dtype == DT_F16 && ids_ok && direct_takes(p)) {
+      const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
+                                                                     : (glu ? p.pairs <= 16
+                                                                            : p.pairs <= p.share || p.pairs <= 8));
+      if (p.glu_out != nullptr) {
+        if (glu || grid_z != 2) return STRATA_ERR_SHAPE;
+        return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
+      }
+      return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
+                 : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);
+    }
+  }
   if constexpr (FastTraits<KIND>::supported) {
     if (x_dtype == DT_F16 && out_dtype == DT_F16 && p.row_ids == nullptr) {
       const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1

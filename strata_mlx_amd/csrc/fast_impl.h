@@ -23,6 +23,7 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 template <int KIND>
 struct FastTraits {
   static constexpr bool supported = false;
+  static constexpr int grid = 0, signs = 0, q2 = 0;
 };
 template <>
 struct FastTraits<K_IQ3_S> {
