@@ -14,6 +14,11 @@ Beside it, on the same line:
   roofline    the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
               (HIP events around a graph of those launches only), against 8 TB/s
   cpu_baseline the oracle's numpy decode + matvec (the reference's CPU path restated) on a few layers
+
+--dense prints only the dense half of a decode token of the mixed model instead (one JSON line): q, k, v 4096 x
+4096 Q6_K, o 4096 x 4096 Q8_0, the shared expert's gate / up 1536 x 4096 and down 4096 x 1536 Q4_K, lm_head
+151936 x 4096 Q6_K (510.5 MB), each through `window_matvec` at one token, as graphs over copies of each
+weight (at least 1 GB a graph, past the MALL).
 """
 
 import argparse
@@ -42,6 +47,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prompt", action="store_true")
+    ap.add_argument("--dense", action="store_true", help="only the dense half of a mixed-model decode token")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 512 MiB with torch's copy kernel three times: the known-size reference that "
                          "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -148,6 +154,41 @@ def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512):
             "hbm_bound_tflops": round(2.0 * tokens * K * 3 * H * F / (3 * E * F * H / 256 * 98) * HBM_PEAK_GBS / 1e3, 1)}
 
 
+DENSE = [("q", "Q6_K", 4096, 4096), ("k", "Q6_K", 4096, 4096), ("v", "Q6_K", 4096, 4096), ("o", "Q8_0", 4096, 4096),
+         ("shared_gate", "Q4_K", 1536, 4096), ("shared_up", "Q4_K", 1536, 4096), ("shared_down", "Q4_K", 4096, 1536),
+         ("lm_head", "Q6_K", 151936, 4096)]
+
+
+def dense_bench(B, synth, dev, steps, warmup):
+    """Each dense matvec of a decode token at one token: mean time over a graph of distinct copies."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    out, total_bytes, total_s = {}, 0, 0.0
+    for name, kind, rows, cols in DENSE:
+        per, bb = synth.DENSE.get(kind) or synth.BLOCK[kind]
+        nbytes = rows * cols // per * bb
+        copies = max(2, -(-(1 << 30) // nbytes))
+        mats = [synth.random_stack(kind, rows * cols, dev, g) for _ in range(copies)]
+        x = (torch.randn((1, cols), device=dev) / 8).half()
+        graph = torch.cuda.CUDAGraph()
+        B.window_matvec(mats[0], kind, rows, cols, x)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            for m in mats:
+                B.window_matvec(m, kind, rows, cols, x)
+        t = time_graph(graph, steps, warmup) / steps / copies
+        out[name] = {"kind": kind, "rows": rows, "cols": cols, "us": round(t * 1e6, 2),
+                     "gbs": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+        total_bytes += nbytes
+        total_s += t
+        del mats
+        torch.cuda.empty_cache()
+    return {"metric": "dense decode matvec GB/s (mixed model, one token)", "value": round(total_bytes / total_s / 1e9, 1),
+            "unit": "GB/s", "us_per_token": round(total_s * 1e6, 1), "bytes_per_token": total_bytes,
+            "hbm_frac": round(total_bytes / total_s / 1e9 / HBM_PEAK_GBS, 4), "dtype": "f16",
+            "data": "synthetic (random blocks)", "layers": out}
+
+
 def cpu_baseline(lins, routes, tokens, budget_s=15.0, max_layers=4):
     """The oracle's numpy decode of the touched experts and their matvecs, one thread, layer by layer until about
     budget_s of CPU work. The experts' bytes are copied to the host first, untimed: the CPU path reads them from
@@ -194,6 +235,11 @@ def main():
 
     def note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    if args.dense:
+        note("dense half of a mixed-model decode token")
+        print(json.dumps(dense_bench(B, synth, dev, max(2, args.steps // 5), 2)))
+        return
 
     if args.copy_probe:
         src = torch.ones(512 << 20, dtype=torch.uint8, device=dev)
