@@ -9,6 +9,7 @@
 //   moe_combine    out = (half)(sum_k y_k * w_k) + (half)((half)sigmoid(g) * s), the experts added in the order
 //                  of strata_mlx/fused.py:448-466 (eight partial sums, expert j into sum j % 8, each product
 //                  rounded before it is added, the sums in order), every half operation rounded once.
+#include <type_traits>
 #include <math.h>
 
 #include <algorithm>
@@ -86,16 +87,27 @@ __device__ __forceinline__ bool beats(float va, uint32_t ia, float vb, uint32_t 
   return va > vb || (va == vb && ia < ib);
 }
 
-// One wave a row of n <= 2048 logits; k <= 64.
+// v from a lane whose index differs in bit d, the other half of an aligned group of 2d lanes (d = 1, 2: quad
+// permutes; 4, 8: the mirror lane within 8 / 16, by DPP; 16, 32: a permute): enough for a butterfly of maxima.
+__device__ __forceinline__ uint32_t across(uint32_t v, int d) {
+  if (d == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);   // quad_perm 1032
+  if (d == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);   // quad_perm 2301
+  if (d == 4) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  if (d == 8) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);  // row_mirror
+  return (uint32_t)__shfl_xor((int)v, d);
+}
+
+// One wave a row of n <= 64 NV logits (NV a lane); k <= 64.
+template <int NV>
 __global__ __launch_bounds__(256) void top_k_kernel(const float* __restrict__ logits, int rows, int n, int k,
                                                     uint32_t* __restrict__ idx, float* __restrict__ weights) {
   const int lane = threadIdx.x % 64;
   const int row = blockIdx.x * kWaves + threadIdx.x / 64;
   if (row >= rows) return;
   const float* lr = logits + (int64_t)row * n;
-  float v[32];
+  float v[NV];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
+  for (int i = 0; i < NV; ++i) {
     const int j = i * 64 + lane;
     v[i] = j < n ? lr[j] : -INFINITY;
   }
@@ -105,16 +117,17 @@ __global__ __launch_bounds__(256) void top_k_kernel(const float* __restrict__ lo
     float best = -INFINITY;
     uint32_t at = 0xffffffffu;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < NV; ++i) {
       const uint32_t j = (uint32_t)(i * 64 + lane);
       if ((int)j < n && beats(v[i], j, best, at)) {
         best = v[i];
         at = j;
       }
     }
-    for (int o = 32; o >= 1; o /= 2) {
-      const float ob = __shfl_xor(best, o);
-      const uint32_t oa = (uint32_t)__shfl_xor((int)at, o);
+#pragma unroll
+    for (int o = 1; o <= 32; o *= 2) {
+      const float ob = __uint_as_float(across(__float_as_uint(best), o));
+      const uint32_t oa = across(at, o);
       if (beats(ob, oa, best, at)) {
         best = ob;
         at = oa;
@@ -126,7 +139,7 @@ __global__ __launch_bounds__(256) void top_k_kernel(const float* __restrict__ lo
     }
     if (at != 0xffffffffu && (int)(at % 64) == lane) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i)
+      for (int i = 0; i < NV; ++i)
         if (i == (int)(at / 64)) v[i] = -INFINITY;
     }
   }
@@ -194,8 +207,17 @@ int strata_top_k(const float* logits, int64_t rows, int64_t n, int64_t k, uint32
   if (!logits || !idx) return STRATA_ERR_ARG;
   if (n > 2048 || k > 64 || k > n || rows > INT32_MAX / 2) return STRATA_ERR_SHAPE;
   const int grid = (int)((rows + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL(top_k_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, logits, (int)rows, (int)n, (int)k,
-                     idx, weights);
+  // the logits a lane holds: the row's length over 64, rounded up to a power of two
+  auto launch = [&](auto nv) {
+    hipLaunchKernelGGL(top_k_kernel<decltype(nv)::value>, dim3(grid), dim3(256), 0, (hipStream_t)stream, logits,
+                       (int)rows, (int)n, (int)k, idx, weights);
+  };
+  if (n <= 64) launch(std::integral_constant<int, 1>{});
+  else if (n <= 128) launch(std::integral_constant<int, 2>{});
+  else if (n <= 256) launch(std::integral_constant<int, 4>{});
+  else if (n <= 512) launch(std::integral_constant<int, 8>{});
+  else if (n <= 1024) launch(std::integral_constant<int, 16>{});
+  else launch(std::integral_constant<int, 32>{});
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }

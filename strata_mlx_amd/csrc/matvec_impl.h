@@ -247,9 +247,22 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* blocks, int
   const int n = (int)(u % runs_per_row);
   float w[32];
   strata_unpack32<KIND>(blocks + r * row_bytes, (uint32_t)n, w, tab);
-  OT* o = out + u * 32;
+  if constexpr (std::is_same<OT, f16>::value) {  // packed pairs, 16-byte stores (64 bytes a run: aligned)
+    u32x4* o4 = reinterpret_cast<u32x4*>(out + u * 32);
 #pragma unroll
-  for (int j = 0; j < 32; ++j) o[j] = from_f32<OT>(w[j]);
+    for (int v = 0; v < 4; ++v) {
+      u32x4 c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        c[i] = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<f16>(w[8 * v + 2 * i])) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<f16>(w[8 * v + 2 * i + 1])) << 16);
+      o4[v] = c;
+    }
+  } else {
+    OT* o = out + u * 32;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[j] = from_f32<OT>(w[j]);
+  }
 }
 
 inline int geometry(MatvecParams& p, int tt_max) {
