@@ -71,9 +71,18 @@ struct RunPair<K_Q6_K> {
   uint32_t d;
 };
 
+template <>
+struct RunPair<K_Q3_K> {
+  u32x4 qs[2];   // the 32 code bytes of the lane's two runs (2 bits a weight, run 2jj + h at bit 4 (jj % 2) + 2h)
+  u32x4 hm[2];   // the 32 high-bit bytes (run r at bit r)
+  uint32_t lo;   // the low four bits of the lane's four 6-bit scales (at bit 4 (jj / 2) of each byte)
+  uint32_t hi;   // their high two bits (at bit 2 jj of each byte)
+  uint32_t d;
+};
+
 template <int KIND>
 struct DirectKind {
-  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K;
+  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K;
   static constexpr bool any = FastTraits<KIND>::supported || linear;
 };
 
@@ -218,6 +227,25 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
     }
     const float d = half_bits(f.d);
     return RunScale{d * (float)(int8_t)(f.sc[h] & 255), d * (float)(int8_t)(f.sc[h] >> 8)};
+  } else if constexpr (KIND == K_Q3_K) {  // w = (q - (hmask bit ? 0 : 4)) * (scale - 32) * d, strata_mlx/blocks.py:164-175
+    const int jj = j & 3, r = 2 * jj + h;  // the block's run
+    const int qsh = 4 * (jj & 1) + 2 * h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t q = (f.qs[i / 4][i % 4] >> qsh) & 0x03030303u;
+      const uint32_t m = (f.hm[i / 4][i % 4] >> r) & 0x01010101u;
+      bytes_to_h2<4>(q | (m << 2), w + 2 * i);
+    }
+    // 6-bit scales 2r and 2r + 1 of the block (strata_mlx/blocks.py:49-53): byte p = 2h, 2h + 1 of the lane's words
+    const float d = half_bits(f.d);
+    float sc[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int p = 2 * h + e;
+      const uint32_t v = ((f.lo >> (8 * p + 4 * (jj >> 1))) & 15) | (((f.hi >> (8 * p + 2 * jj)) & 3) << 4);
+      sc[e] = d * (float)((int)v - 32);
+    }
+    return RunScale{sc[0], sc[1]};
   } else {
     return RunScale{decode_pair<KIND>(f, h, w, t), 0.0f};
   }
@@ -243,7 +271,7 @@ __device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w,
                                0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
                                0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
     return s.a * dot16x2(w, x) - s.b * dot_n<16>(ones, x);
-  } else if constexpr (KIND == K_Q6_K) {
+  } else if constexpr (KIND == K_Q6_K || KIND == K_Q3_K) {  // a scale every 16 weights
     return s.a * dot_n<8>(w, x) + s.b * dot_n<8>(w + 8, x + 8);
   } else {
     return s.a * dot16x2(w, x);
@@ -304,6 +332,9 @@ __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
     asm volatile("" : "+v"(f.ql[0]), "+v"(f.ql[1]), "+v"(f.qh[0]), "+v"(f.qh[1]), "+v"(f.sc[0]), "+v"(f.sc[1]),
                  "+v"(f.d));
     return;
+  } else if constexpr (KIND == K_Q3_K) {
+    asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.hm[0]), "+v"(f.hm[1]), "+v"(f.lo), "+v"(f.hi), "+v"(f.d));
+    return;
   } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(f.qs[i]));
@@ -358,6 +389,13 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.d = b;
     o.qs = b + 16 + 32 * jj;
     o.a = b + 4;
+  } else if constexpr (KIND == K_Q3_K) {  // hmask[32] @0, qs[64] @32, scales[12] @96, d @108
+    const uint32_t b = (j >> 2) * 110, jj = j & 3;
+    o.d = b + 108;
+    o.qs = b + 32 + 32 * (jj >> 1);
+    o.a = b;
+    o.b = b + 96 + 4 * (jj & 1);
+    o.c = b + 104;
   } else if constexpr (KIND == K_Q6_K) {  // ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208
     const uint32_t b = (j >> 2) * 210, hh = (j >> 1) & 1, r0 = j & 1;
     o.d = b + 208;
@@ -403,6 +441,15 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
     f.sm = load_at<u32x4>(row, lo + o.a);
     f.qs[0] = load_at<u32x4>(row, lo + o.qs);
     f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    return;
+  } else if constexpr (KIND == K_Q3_K) {
+    f.d = load_at<uint16_t>(row, lo + o.d);
+    f.lo = load_at<uint32_t>(row, lo + o.b);
+    f.hi = load_at<uint32_t>(row, lo + o.c);
+    f.qs[0] = load_at<u32x4>(row, lo + o.qs);
+    f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    f.hm[0] = load_at<u32x4>(row, lo + o.a);
+    f.hm[1] = load_at<u32x4>(row, lo + o.a + 16);
     return;
   } else if constexpr (KIND == K_Q6_K) {
     f.d = load_at<uint16_t>(row, lo + o.d);

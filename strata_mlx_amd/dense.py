@@ -17,7 +17,9 @@ import torch
 from . import blocks as B
 
 MAX_TOKENS = 8  # more than a window: a chunk of a prompt, multiplied as floats (dense.py:33)
-PLANES = True  # Q3_K layers held as planes (blocks.q3k_planes), as the reference holds them (dense.py:190, 214-215)
+# Q3_K layers held as planes (blocks.q3k_planes), as the reference holds them (dense.py:190, 214-215), when True;
+# by default they stay the file's blocks, which the register decode reads at twice the planes window's speed
+PLANES = False
 
 
 def q6k_blocks(codes: torch.Tensor, scales: torch.Tensor, d: torch.Tensor) -> torch.Tensor:

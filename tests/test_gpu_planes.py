@@ -1,7 +1,8 @@
 """Q3_K held as planes on the GPU (strata_mlx/blocks.py:397-512) against the oracle: the planes are the oracle's
 rearrangement bit for bit, their dequantization the oracle's Q3_K weights bit for bit, the window's products the
 float64 product at the reference's tolerances (test_dense.py:49: 2e-5 float32, 4e-3 float16, relative to the
-largest output), a token alone the bits it gets in a window, and BlockLinear over Q3_K holds planes."""
+largest output), a token alone the bits it gets in a window, and BlockLinear over Q3_K holds planes when asked
+to (else the file's blocks)."""
 
 import numpy as np
 import pytest
@@ -53,11 +54,20 @@ def test_the_window_is_the_product(gpu, tokens, dtype):
     assert torch.equal(alone.cpu()[0], B.q3k_planes_window(planes, rows, cols, x.to(gpu)).cpu()[-1])
 
 
-def test_block_linear_holds_q3_k_as_planes(gpu):
+@pytest.mark.parametrize("planes", [True, False])
+def test_block_linear_holds_q3_k_as_planes_or_blocks(gpu, planes, monkeypatch):
+    monkeypatch.setattr(D, "PLANES", planes)
     rng = np.random.default_rng(6)
     rows, cols = 40, 1024
     data = O.random_blocks("Q3_K", rows * cols // 256, rng)
     layer = D.BlockLinear(dev(data, gpu), "Q3_K", (rows, cols))
+    if not planes:
+        assert layer.planes is None and layer.nbytes == rows * cols // 256 * 110
+        x = torch.randn((3, cols), generator=torch.Generator().manual_seed(2))
+        got = layer(x.half().to(gpu)).float().cpu().numpy()
+        want = x.half().double().numpy() @ O.dequantize(data, "Q3_K", (rows, cols)).astype(np.float64).T
+        assert np.abs(got - want).max() <= 4e-3 * np.abs(want).max()
+        return
     assert layer.planes is not None and layer.nbytes == rows * cols // 256 * B.Q3K_PLANE_BYTES
     x = torch.randn((20, cols), generator=torch.Generator().manual_seed(2))  # more than a window: floats
     got = layer(x.to(gpu)).cpu().numpy()
