@@ -33,21 +33,21 @@ struct RunPair;
 template <>
 struct RunPair<K_IQ3_S> {
   u32x4 qs;     // 16 index bytes
-  uint32_t qh;  // two high-bit bytes
+  uint16_t qh;  // two high-bit bytes
   u32x2 sg;     // eight sign bytes
-  uint32_t sc;  // the scale byte: low nibble the first run's, high the second's
-  uint32_t d;
+  uint16_t sc;  // the block's scale bytes 2 (j % 4 / 2), + 1: byte j % 2 the lane's (low nibble run 2j's)
+  uint16_t d;
 };
 template <>
 struct RunPair<K_IQ3_XXS> {
   u32x4 qs;
   u32x2 aux;    // the two runs' scale and sign words
-  uint32_t d;
+  uint16_t d;
 };
 template <>
 struct RunPair<K_Q2_0> {
   u32x4 qs;     // the block's 16 code bytes
-  uint32_t d;
+  uint16_t d;
 };
 // The kinds decoded without a codebook: a lane's 64 weights are two Q8_0 blocks, a quarter of a Q4_K block (the
 // low and high nibbles of 32 bytes), or two runs of a Q6_K half block (r0 and r0 + 2: the low and high nibbles of
@@ -55,7 +55,7 @@ struct RunPair<K_Q2_0> {
 template <>
 struct RunPair<K_Q8_0> {
   u32x4 q[4];   // the two blocks' 32 int8 codes each
-  uint32_t d[2];
+  uint16_t d[2];
 };
 template <>
 struct RunPair<K_Q4_K> {
@@ -67,8 +67,8 @@ template <>
 struct RunPair<K_Q6_K> {
   u32x4 ql[2];     // 32 bytes: run r0's low four bits in the low nibbles, run r0 + 2's in the high
   u32x4 qh[2];     // the half's 32 high-bit bytes
-  uint32_t sc[2];  // each run's two int8 scales (16 weights a scale)
-  uint32_t d;
+  uint16_t sc[2];  // each run's two int8 scales (16 weights a scale)
+  uint16_t d;
 };
 
 template <>
@@ -77,7 +77,7 @@ struct RunPair<K_Q3_K> {
   u32x4 hm[2];   // the 32 high-bit bytes (run r at bit r)
   uint32_t lo;   // the low four bits of the lane's four 6-bit scales (at bit 4 (jj / 2) of each byte)
   uint32_t hi;   // their high two bits (at bit 2 jj of each byte)
-  uint32_t d;
+  uint16_t d;
 };
 
 template <int KIND>
@@ -99,32 +99,6 @@ __device__ __forceinline__ T load_unaligned(const uint8_t* p) {
 
 __device__ __forceinline__ float half_bits(uint32_t b) { return (float)__builtin_bit_cast(f16, (uint16_t)b); }
 
-// run pair j of a row (runs 2j, 2j + 1)
-template <int KIND>
-__device__ __forceinline__ void load_pair(const uint8_t* row, int j, RunPair<KIND>& f) {
-  if constexpr (KIND == K_IQ3_S) {  // d @0, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106
-    const uint8_t* b = row + (j >> 2) * 110;
-    const int ib0 = 2 * (j & 3);
-    f.d = load_unaligned<uint16_t>(b);
-    f.qs = load_unaligned<u32x4>(b + 2 + 8 * ib0);
-    f.qh = load_unaligned<uint16_t>(b + 66 + ib0);
-    f.sg = load_unaligned<u32x2>(b + 74 + 4 * ib0);
-    f.sc = load_unaligned<uint8_t>(b + 106 + (j & 3));
-  } else if constexpr (KIND == K_IQ3_XXS) {  // d @0, qs[64] @2, aux[8] (u32) @66
-    const uint8_t* b = row + (j >> 2) * 98;
-    const int ib0 = 2 * (j & 3);
-    f.d = load_unaligned<uint16_t>(b);
-    f.qs = load_unaligned<u32x4>(b + 2 + 8 * ib0);
-    f.aux = load_unaligned<u32x2>(b + 66 + 4 * ib0);
-  } else if constexpr (DirectKind<KIND>::linear) {
-    static_assert(KIND != KIND, "the linear kinds load through load_fields");
-  } else {  // Q2_0: d @0, qs[16] @2
-    const uint8_t* b = row + j * 18;
-    f.d = load_unaligned<uint16_t>(b);
-    f.qs = load_unaligned<u32x4>(b + 2);
-  }
-}
-
 // The LDS tables of the register decode: codebook entries as four float16 integers, and the XOR masks of four
 // sign bits (16 entries of 8 bytes: one row of banks, so lanes reading different entries never conflict).
 template <int KIND>
@@ -136,12 +110,13 @@ struct DirectTables {
 
 // run h (0, 1) of a pair: 16 packed float16 pairs of integers, and the run's scale
 template <int KIND>
-__device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, uint32_t* w, const DirectTables<KIND>& t) {
+__device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, int j, uint32_t* w,
+                                             const DirectTables<KIND>& t) {
   const float d = half_bits(f.d);
   if constexpr (KIND == K_IQ3_S) {  // strata_mlx/blocks.py:89-102
     const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
     const uint32_t qh = (f.qh >> (8 * h)) & 255, sg = f.sg[h];
-    const float scale = d * (float)(1 + 2 * ((f.sc >> (4 * h)) & 15));
+    const float scale = d * (float)(1 + 2 * __builtin_amdgcn_ubfe((uint32_t)f.sc, 8 * (j & 1) + 4 * h, 4));
     // the ninth index bits of four groups spread into bytes, then interleaved with the qs bytes by v_perm
     const uint32_t hb0 = (__builtin_amdgcn_ubfe(qh, 0, 4) * 0x204081u) & 0x01010101u;
     const uint32_t hb1 = (__builtin_amdgcn_ubfe(qh, 4, 4) * 0x204081u) & 0x01010101u;
@@ -247,7 +222,7 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
     }
     return RunScale{sc[0], sc[1]};
   } else {
-    return RunScale{decode_pair<KIND>(f, h, w, t), 0.0f};
+    return RunScale{decode_pair<KIND>(f, h, j, w, t), 0.0f};
   }
 }
 
@@ -347,6 +322,14 @@ __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
   }
 }
 
+// The loads of these 32 registers are complete here (the compiler waits for them before this point).
+__device__ __forceinline__ void arrived(uint32_t (&v)[32]) {
+#pragma unroll
+  for (int i = 0; i < 32; i += 8)
+    asm volatile("" : "+v"(v[i]), "+v"(v[i + 1]), "+v"(v[i + 2]), "+v"(v[i + 3]), "+v"(v[i + 4]), "+v"(v[i + 5]),
+                 "+v"(v[i + 6]), "+v"(v[i + 7]));
+}
+
 // the lowest pair left in the four masks, taken out; -1 when none is
 __device__ __forceinline__ int take_lowest(uint64_t& m) {
   const int b = __ffsll((unsigned long long)m) - 1;
@@ -375,7 +358,7 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.qs = b + 2 + 16 * jj;
     o.a = b + 66 + 2 * jj;
     o.b = b + 74 + 8 * jj;
-    o.c = b + 106 + jj;
+    o.c = b + 106 + 2 * (jj >> 1);
   } else if constexpr (KIND == K_IQ3_XXS) {  // d @0, qs[64] @2, aux[8] (u32) @66
     const uint32_t b = (j >> 2) * 98, jj = j & 3;
     o.d = b;
@@ -466,7 +449,7 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
   if constexpr (KIND == K_IQ3_S) {
     f.qh = load_at<uint16_t>(row, lo + o.a);
     f.sg = load_at<u32x2>(row, lo + o.b);
-    f.sc = load_at<uint8_t>(row, lo + o.c);
+    f.sc = load_at<uint16_t>(row, lo + o.c);
   } else if constexpr (KIND == K_IQ3_XXS) {
     f.aux = load_at<u32x2>(row, lo + o.a);
   }
@@ -585,6 +568,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
     }
     const uint8_t* row = (PAIRED && (s & 1) ? m1 : m0) + (int64_t)rw * p.row_bytes;
     load_fields<KIND>(row, (uint32_t)(rl - rw) * p.row_bytes, lo, f[s]);
+    asm volatile("" ::: "memory");  // the steps' loads go out in step order: step 0 is decoded first
   }
   if constexpr (GLU) {  // silu(gate) * up waits for its loads: after the rows' have gone out
     fast_load_x<true>(p, q0, run_of<KIND>(jp, 0), x[0]);
@@ -662,13 +646,20 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
       }
     }
     if (nq == 0) break;
+    if constexpr (GLU) {  // its activations are loaded after the rows: every row step is waited for at once
 #pragma unroll
-    for (int st = 0; st < RU; ++st) opaque(f[st]);  // decoded anew each pass, not hoisted out of the loop
+      for (int st = 0; st < RU; ++st) opaque(f[st]);
+    }
+    // A pass's other activations are waited for where they are loaded. A load still in flight past this branch
+    // would be counted by every later wait, on the first pass too, and step 0's decode would then wait for all
+    // the row loads; as it is, the wait before each row step's decode counts only the row loads after that
+    // step's, and step 0 is decoded while the later steps' bytes are still arriving.
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       if (t < nq && (pass > 0 || t > 0)) {
         fast_load_x<GLU>(p, q[t], run_of<KIND>(jp, 0), x[t]);
         fast_load_x<GLU>(p, q[t], run_of<KIND>(jp, 1), x[t] + 16);
+        arrived(x[t]);
       }
     }
     float acc[TT][RU];
@@ -678,6 +669,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
       const int r = r0 + (PAIRED ? s / 2 : s) * side + sub;
 #pragma unroll
       for (int t = 0; t < TT; ++t) acc[t][s] = 0.0f;
+      if constexpr (!GLU) opaque(f[s]);  // decoded anew each pass, each step once its own loads are in
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         uint32_t w[16];
