@@ -400,6 +400,16 @@ __device__ __forceinline__ int run_of(int j, int h) {
   return 2 * j + h;
 }
 
+// Where 16-byte piece c of the activations sits in LDS. A lane reads the 8 pieces of its own 128 bytes, so
+// without a swizzle every lane of a read starts on the same bank; the low three bits of c are XORed with a key
+// of its lane (c / 8) that differs between any 8 consecutive lanes, and between the lanes of each parity among
+// 16 consecutive lanes, so the lanes of one LDS cycle of a 16-byte read (8 at 128 bytes a clock, 16 at 256)
+// fall on distinct banks. A bijection within each 8 pieces.
+__device__ __forceinline__ int x_slot(int c) {
+  const int j = c >> 3;
+  return c ^ (((j >> 1) & 7) ^ ((j & 1) << 2));
+}
+
 // A load at base + off: base the same for the whole wave, off the lane's (global_load v, v_off, s_base).
 template <typename T>
 __device__ __forceinline__ T load_at(const uint8_t* base, uint32_t off) {
@@ -469,11 +479,15 @@ __device__ __forceinline__ float lanes_apart(float v, int d) {
 }
 
 // N partial sums a lane (N row steps) over rows of L lanes -> the lanes of group ln / (L / N) hold the total of
-// row step ln / (L / N). Exchange halves first (N - 1 moves), then reduce the one value left (log2(L / N)).
+// row step ln / (L / N). Exchange halves first (N - 1 moves), then reduce the one value left (log2(L / N)). The
+// loops count up to a constant, so they unroll and every index is known (a run-time index would put the sums in
+// scratch memory).
 template <int L, int N>
 __device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
+  constexpr int kHalvings = N >= 8 ? 3 : N >= 4 ? 2 : N >= 2 ? 1 : 0;
 #pragma unroll
-  for (int n = N, d = L / 2; n > 1; n /= 2, d /= 2) {
+  for (int k = 0; k < kHalvings; ++k) {
+    const int n = N >> k, d = (L / 2) >> k;
     const bool up = (ln & d) != 0;
 #pragma unroll
     for (int i = 0; i < n / 2; ++i) {
@@ -583,7 +597,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   if (shared_x) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
-      if (tid + k * kThreads < p.cols / 8) xs[tid + k * kThreads] = xv[k];
+      if (tid + k * kThreads < p.cols / 8) xs[x_slot(tid + k * kThreads)] = xv[k];
   }
   if (p.mode == MODE_EXPERT && !bad) {
     bool earlier = false;
@@ -606,7 +620,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   if (shared_x) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const u32x4 c = xs[4 * run_of<KIND>(jp, v / 4) + v % 4];
+      const u32x4 c = xs[x_slot(4 * run_of<KIND>(jp, v / 4) + v % 4)];
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[0][4 * v + i] = c[i];
     }
