@@ -26,6 +26,7 @@ namespace strata_mv {
 
 constexpr int kDMaxPairs = 256;  // pairs the direct kernel takes (four ballots)
 constexpr int kDMaxCols = 4096;  // inputs of a row the direct kernel takes (64 lanes of 64)
+constexpr int kDMaxGridY = 65535;  // pairs (and stacks) of a launch: the grid's y and z
 
 // the fields of two consecutive runs of a block, as one lane holds them
 template <int KIND>
@@ -400,14 +401,22 @@ __device__ __forceinline__ int run_of(int j, int h) {
   return 2 * j + h;
 }
 
-// Where 16-byte piece c of the activations sits in LDS. A lane reads the 8 pieces of its own 128 bytes, so
-// without a swizzle every lane of a read starts on the same bank; the low three bits of c are XORed with a key
-// of its lane (c / 8) that differs between any 8 consecutive lanes, and between the lanes of each parity among
-// 16 consecutive lanes, so the lanes of one LDS cycle of a 16-byte read (8 at 128 bytes a clock, 16 at 256)
-// fall on distinct banks. A bijection within each 8 pieces.
-__device__ __forceinline__ int x_slot(int c) {
-  const int j = c >> 3;
-  return c ^ (((j >> 1) & 7) ^ ((j & 1) << 2));
+// One token's activations in LDS: lane j's two runs (h = 0, 1) as 16-byte pieces 17 j + 4 h + i (i the piece
+// within the run), so a lane's 128 bytes are contiguous and lanes sit 272 bytes apart: the 8 (16) lanes served
+// in one cycle of a 16-byte LDS read fall on distinct banks at 128 (256) bytes a clock.
+constexpr int kXPitch = 17;  // 16-byte slots a lane
+template <int KIND>
+__device__ __forceinline__ int x_slot(int c) {  // the slot of piece c of the row (c / 4: the run)
+  const int r = c >> 2, i = c & 3;
+  int j, h;  // the lane and half that multiply run r: the inverse of run_of
+  if constexpr (KIND == K_Q6_K) {
+    j = 4 * (r >> 3) + 2 * ((r >> 2) & 1) + (r & 1);
+    h = (r >> 1) & 1;
+  } else {
+    j = r >> 1;
+    h = r & 1;
+  }
+  return kXPitch * j + 4 * h + i;
 }
 
 // A load at base + off: base the same for the whole wave, off the lane's (global_load v, v_off, s_base).
@@ -503,13 +512,14 @@ __device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
 }
 
 // Unit geometry: L lanes to a row (LT when known at compile time, else p.ct), p.rt rows of each matrix a unit,
-// p.ntiles units to a matrix, p.nz stacks taken as separate units (1 in paired mode), p.items units in all.
+// p.ntiles units to a matrix; the grid is (units of a matrix / kWaves, stacks taken as separate units (1 in
+// paired mode), pairs), so a wave finds its unit without a division.
 // Every load before the first wait has no branch around it: rows past the end and lanes past a row's run
 // pairs load the last row / run pair again, and an expert id out of range loads expert 0's rows and writes NaN.
 template <int KIND, bool GLU, bool PAIRED, int TT, int RU, int LT>
 __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kernel(MatvecParams p) {
   __shared__ DirectTables<KIND> tab;
-  __shared__ u32x4 xs[kDMaxCols / 8];  // one token's activations, when every wave multiplies the same token
+  __shared__ u32x4 xs[kXPitch * (kDMaxCols / 64)];  // one token's activations, when every wave multiplies it
   const int tid = threadIdx.x, lane = tid % 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
   const int L = LT > 0 ? LT : p.ct;
@@ -520,13 +530,10 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   const int jp = min(ln, npr - 1);
   constexpr int kSteps = PAIRED ? RU / 2 : RU;  // row steps of each matrix
 
-  const int unit = blockIdx.x * kWaves + wave;
-  const bool in_range = unit < p.items;
-  const int u = in_range ? unit : 0;
-  const int per_pair = p.nz * p.ntiles;
-  const int pair = u / per_pair, rem = u % per_pair;
-  const int z0 = rem / p.ntiles;
-  const int r0 = (rem % p.ntiles) * p.rt;
+  const int tile = blockIdx.x * kWaves + wave;
+  const bool in_range = tile < p.ntiles;
+  const int pair = blockIdx.z, z0 = blockIdx.y;
+  const int r0 = (in_range ? tile : 0) * p.rt;
 
   const uint8_t* m0;
   const uint8_t* m1 = nullptr;
@@ -597,7 +604,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   if (shared_x) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
-      if (tid + k * kThreads < p.cols / 8) xs[x_slot(tid + k * kThreads)] = xv[k];
+      if (tid + k * kThreads < p.cols / 8) xs[x_slot<KIND>(tid + k * kThreads)] = xv[k];
   }
   if (p.mode == MODE_EXPERT && !bad) {
     bool earlier = false;
@@ -620,7 +627,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   if (shared_x) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const u32x4 c = xs[x_slot(4 * run_of<KIND>(jp, v / 4) + v % 4)];
+      const u32x4 c = xs[kXPitch * jp + v];
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[0][4 * v + i] = c[i];
     }
@@ -791,11 +798,10 @@ int launch_direct_ru(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream
   p.nz = PAIRED ? 1 : grid_z;
   p.rt = (PAIRED ? RU / 2 : RU) * side;
   p.ntiles = (p.rows + p.rt - 1) / p.rt;
-  const int64_t units = (int64_t)grid_y * p.nz * p.ntiles;
-  if (units > INT32_MAX - kWaves) return STRATA_ERR_SHAPE;
-  p.items = (int)units;
-  const int grid = (int)((units + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL((direct_decode_kernel<KIND, GLU, PAIRED, TT, RU, LT>), dim3(grid), dim3(kThreads), 0, stream, p);
+  if (grid_y > kDMaxGridY || p.nz > kDMaxGridY) return STRATA_ERR_SHAPE;
+  p.items = p.ntiles;
+  const dim3 grid((p.ntiles + kWaves - 1) / kWaves, p.nz, grid_y);
+  hipLaunchKernelGGL((direct_decode_kernel<KIND, GLU, PAIRED, TT, RU, LT>), grid, dim3(kThreads), 0, stream, p);
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }
@@ -815,7 +821,8 @@ int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
   if constexpr (DirectKind<KIND>::linear) {  // their wider fields spill at four row steps
     return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
   } else {
-    if (row_steps() == 2 || (KIND == K_Q2_0 && TT > 1)) return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
+    if (row_steps() == 2 || (KIND == K_Q2_0 && TT > 1))
+      return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
     return launch_direct_lt<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
   }
 }
@@ -823,7 +830,8 @@ int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
 // Rows of 64 to 4096 weights in run pairs (every IQ3_S / IQ3_XXS / Q2_0 row), up to 256 pairs.
 inline bool direct_takes(const MatvecParams& p) {
   const int runs = p.cols / 32;
-  return runs % 2 == 0 && runs >= 2 && runs / 2 <= 64 && (p.mode != MODE_EXPERT || p.pairs <= kDMaxPairs);
+  return runs % 2 == 0 && runs >= 2 && runs / 2 <= 64 && (p.mode != MODE_EXPERT || p.pairs <= kDMaxPairs) &&
+         (p.mode != MODE_PTRS || p.pairs <= kDMaxGridY);
 }
 
 template <int KIND, bool GLU, bool PAIRED>
