@@ -475,23 +475,49 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
   }
 }
 
-// v from the lane whose index differs in bit d (d = 1, 2, 4, 8: DPP within rows of 16; 16, 32: permute). For
+// gfx950's row swaps between two registers: d = 16 exchanges the odd rows of 16 lanes of the first with the even
+// rows of the second (v_permlane16_swap), d = 32 the upper 32 lanes of the first with the lower 32 of the second
+// (v_permlane32_swap). Returns the two registers after the swap.
+__device__ __forceinline__ void swap_rows(float a, float b, int d, float& a2, float& b2) {
+  const auto r = d == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false)
+                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a2 = __uint_as_float(r[0]);
+  b2 = __uint_as_float(r[1]);
+}
+
+// v from the lane whose index differs in bit d (d = 1, 2, 4, 8: DPP within rows of 16; 16, 32: a row swap). For
 // d = 4 and 8 the partner is the mirror lane within 8 / 16 lanes, which also differs in bit d: a reduction or an
 // exchange between the two halves needs only that.
+template <bool SWAP = false>
 __device__ __forceinline__ float lanes_apart(float v, int d) {
   const int b = __float_as_int(v);
   if (d == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false));   // quad_perm 1032
   if (d == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false));   // quad_perm 2301
   if (d == 4) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x141, 0xF, 0xF, false));  // row_half_mirror
   if (d == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x140, 0xF, 0xF, false));  // row_mirror
+  if (SWAP && (d == 16 || d == 32)) {  // after swapping v with itself: the first copy the lower rows', the second the upper's
+    float lo, hi;
+    swap_rows(v, v, d, lo, hi);
+    const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    return (lane & d) ? lo : hi;
+  }
   return __shfl_xor(v, d);
+}
+
+// a + a' where bit d of the lane is clear, b + b' where it is set (a', b': the registers of the lane whose index
+// differs in bit d), for d = 16, 32: a row swap of a with b puts a's upper rows beside its lower ones and b's lower
+// rows beside its upper ones, so the sum of the two registers after the swap is the answer in every lane.
+__device__ __forceinline__ float sum_swapped(float a, float b, int d) {
+  float a2, b2;
+  swap_rows(a, b, d, a2, b2);
+  return a2 + b2;
 }
 
 // N partial sums a lane (N row steps) over rows of L lanes -> the lanes of group ln / (L / N) hold the total of
 // row step ln / (L / N). Exchange halves first (N - 1 moves), then reduce the one value left (log2(L / N)). The
 // loops count up to a constant, so they unroll and every index is known (a run-time index would put the sums in
-// scratch memory).
-template <int L, int N>
+// scratch memory). SWAP: row swaps for d = 16, 32 (with two tokens a pass they push the kernel into spills).
+template <int L, int N, bool SWAP>
 __device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
   constexpr int kHalvings = N >= 8 ? 3 : N >= 4 ? 2 : N >= 2 ? 1 : 0;
 #pragma unroll
@@ -500,6 +526,10 @@ __device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
     const bool up = (ln & d) != 0;
 #pragma unroll
     for (int i = 0; i < n / 2; ++i) {
+      if (SWAP && d >= 16) {
+        v[i] = sum_swapped(v[i], v[i + n / 2], d);
+        continue;
+      }
       const float send = up ? v[i] : v[i + n / 2];
       const float keep = up ? v[i + n / 2] : v[i];
       v[i] = keep + lanes_apart(send, d);
@@ -507,7 +537,7 @@ __device__ __forceinline__ float reduce_steps(float (&v)[N], int ln) {
   }
   float s = v[0];
 #pragma unroll
-  for (int d = L / N / 2; d >= 1; d /= 2) s += lanes_apart(s, d);
+  for (int d = L / N / 2; d >= 1; d /= 2) s = SWAP && d >= 16 ? sum_swapped(s, s, d) : s + lanes_apart(s, d);
   return s;
 }
 
@@ -718,11 +748,11 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nq) continue;
-        const float v = reduce_steps<LT, RU>(acc[t], ln);
+        const float v = reduce_steps<LT, RU, TT == 1>(acc[t], ln);
         float h = 0.0f;
         f16 gq, uq;
         if constexpr (PAIRED) {  // gate in group 2k, up in group 2k + 1
-          const float up = lanes_apart(v, G);
+          const float up = lanes_apart<TT == 1>(v, G);
           gq = from_f32<f16>(v);
           uq = from_f32<f16>(up);
           h = swiglu_rounded<f16>(gq, uq);
