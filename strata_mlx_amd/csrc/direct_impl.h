@@ -857,6 +857,159 @@ int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
   }
 }
 
+// Rows of 8 S run pairs for odd S (S = 3: 1536 inputs, the down projection of a 4096 x 1536 expert; S = 5: 2560)
+// fill the power-of-two rows of direct_decode_kernel badly: 24 run pairs on 32 lanes leave a quarter of the lanes
+// idle. Here 8 lanes take a row and lane m takes its run pairs m, m + 8, ... (S steps of eight consecutive run
+// pairs, every lane busy), so a wave holds 8 rows, and a row's sum meets over 8 lanes by three DPP steps. The
+// lane's activations differ from step to step: the pair's token sits in LDS (one copy for the workgroup, whose
+// waves all multiply the same pair) and each step reads its 128 bytes. Routed pairs or a matrix a pair, one token
+// a pass.
+template <int KIND, int S>
+__global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(MatvecParams p) {
+  constexpr int kPairs = 8 * S;     // run pairs of a row
+  constexpr int kPieces = 8 * kPairs;  // 16-byte pieces of a token
+  __shared__ DirectTables<KIND> tab;
+  __shared__ u32x4 xs[kXPitch * kPairs];
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int m = lane & 7, sub = lane >> 3;  // run pairs m, m + 8, ... of row sub
+  const int tile = blockIdx.x * kWaves + wave;
+  const bool in_range = tile < p.ntiles;
+  const int pair = blockIdx.z, z0 = blockIdx.y;
+  const int r0 = (in_range ? tile : 0) * 8;
+  const int row = min(r0 + sub, p.rows - 1);
+  const bool routed = p.mode == MODE_EXPERT;
+  const uint32_t expert = routed ? p.idx[pair] : 0u;
+  const bool bad = routed && expert >= (uint64_t)p.experts;
+  const uint8_t* m0 = routed ? p.blocks[z0] + (int64_t)(bad ? 0u : expert) * p.mat_bytes : p.ptrs[pair];
+
+  // loads in the order they are waited for: the tables' constants and the pairs' ids, the token, the rows
+  TableFetch<KIND> tf;
+  fetch_tables<KIND>(tf, tid);
+  uint32_t e[4] = {0, 0, 0, 0};
+  if (routed) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
+  }
+  const bool one_x = routed && p.share == p.pairs;  // every pair the same token: one pass writes them all
+  u32x4 xv[(kPieces + kThreads - 1) / kThreads];
+  const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(p.x) + (int64_t)(pair / p.share) * p.cols);
+#pragma unroll
+  for (int k = 0; k * kThreads < kPieces; ++k) xv[k] = src[min(tid + k * kThreads, kPieces - 1)];
+  RunPair<KIND> f[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    load_fields<KIND>(m0, (uint32_t)row * (uint32_t)p.row_bytes, lane_offsets<KIND>(8 * s + m), f[s]);
+    asm volatile("" ::: "memory");  // the steps' loads go out in step order: step 0 is decoded first
+  }
+  asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(tf.g[0]), "+v"(tf.g[1])::"memory");
+  store_tables<KIND>(tab, tf, tid);
+#pragma unroll
+  for (int k = 0; k * kThreads < kPieces; ++k)
+    if (tid + k * kThreads < kPieces) xs[x_slot<KIND>(tid + k * kThreads)] = xv[k];
+  // the pairs naming this expert from this one on (a matrix a pair: this pair); the same for every wave of the
+  // workgroup (one pair)
+  uint64_t mb[4] = {0, 0, 0, 0};
+  bool earlier = false;
+  if (!routed) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) mb[c] = pair / 64 == c ? 1ull << (pair % 64) : 0ull;
+  } else if (!bad) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint64_t b = __ballot(64 * c + lane < p.pairs && e[c] == expert);
+      const int lo_bits = pair - 64 * c;  // bits below are earlier pairs
+      const uint64_t below = lo_bits <= 0 ? 0ull : (lo_bits >= 64 ? ~0ull : ((1ull << lo_bits) - 1));
+      earlier |= (b & below) != 0;
+      mb[c] = b & ~below;
+    }
+  }
+  __syncthreads();
+  if (earlier) return;  // an earlier pair's waves multiply these rows
+  if (bad) {  // a pair naming no expert: NaN
+    if (m == 0 && in_range && r0 + sub < p.rows)
+      reinterpret_cast<f16*>(p.out[z0])[(int64_t)pair * p.rows + r0 + sub] = (f16)__builtin_nanf("");
+    return;
+  }
+  for (int pass = 0;; ++pass) {
+    const int q = take_member(mb[0], mb[1], mb[2], mb[3]);  // this pass's pair (the first: this one)
+    if (q < 0) break;
+    if (pass > 0) {  // the next pair's token into LDS, once every wave is done with the last one
+      const u32x4* sq = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(p.x) + (int64_t)(q / p.share) * p.cols);
+#pragma unroll
+      for (int k = 0; k * kThreads < kPieces; ++k) xv[k] = sq[min(tid + k * kThreads, kPieces - 1)];
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k * kThreads < kPieces; ++k)
+        if (tid + k * kThreads < kPieces) xs[x_slot<KIND>(tid + k * kThreads)] = xv[k];
+      __syncthreads();
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      opaque(f[s]);  // decoded anew each pass, each step once its own loads are in
+      const int j = 8 * s + m;
+      uint32_t x[32];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const u32x4 c = xs[kXPitch * j + v];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t w[16];
+        const RunScale rs = decode_run<KIND>(f[s], h, j, w, tab);
+        acc += apply_run<KIND>(rs, w, x + 16 * h);
+      }
+    }
+    acc += lanes_apart(acc, 1);
+    acc += lanes_apart(acc, 2);
+    acc += lanes_apart(acc, 4);
+    if (m == 0 && in_range && r0 + sub < p.rows) {  // this pass's pair, or (one token) every pair naming the expert
+      const f16 v = from_f32<f16>(acc);
+      f16* out = reinterpret_cast<f16*>(p.out[z0]) + r0 + sub;
+      out[(int64_t)q * p.rows] = v;
+      uint64_t a0 = mb[0], a1 = mb[1], a2 = mb[2], a3 = mb[3];
+      if (one_x)
+        for (int qq = take_member(a0, a1, a2, a3); qq >= 0; qq = take_member(a0, a1, a2, a3)) out[(int64_t)qq * p.rows] = v;
+    }
+    if (one_x) break;
+  }
+}
+
+// Rows of 24 or 40 run pairs (1536, 2560 inputs), routed pairs or a matrix a pair, one token a pass:
+// direct_odd_kernel.
+template <int KIND>
+int launch_direct_odd(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
+  const int pairs = p.cols / 64;
+  if (grid_y > kDMaxGridY || grid_z > kDMaxGridY || (int64_t)p.rows * p.row_bytes >= ((int64_t)1 << 32))
+    return STRATA_ERR_SHAPE;
+  p.nz = grid_z;
+  p.ntiles = (p.rows + 7) / 8;
+  p.items = p.ntiles;
+  const dim3 grid((p.ntiles + kWaves - 1) / kWaves, grid_z, grid_y);
+  if (pairs == 24) {
+    hipLaunchKernelGGL((direct_odd_kernel<KIND, 3>), grid, dim3(kThreads), 0, stream, p);
+  } else if (pairs == 40) {
+    hipLaunchKernelGGL((direct_odd_kernel<KIND, 5>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    return STRATA_ERR_SHAPE;
+  }
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
+inline bool odd_takes(const MatvecParams& p) {
+  static const bool on = [] {  // STRATA_ODD_ROWS=0: such rows take direct_decode_kernel (to compare)
+    const char* e = getenv("STRATA_ODD_ROWS");
+    return !(e && e[0] == '0');
+  }();
+  return on && p.cols % 64 == 0 && (p.cols / 64 == 24 || p.cols / 64 == 40) &&
+         (p.mode == MODE_EXPERT || p.mode == MODE_PTRS) && p.pairs <= kDMaxPairs && p.row_ids == nullptr &&
+         p.glu_out == nullptr;
+}
+
 // Rows of 64 to 4096 weights in run pairs (every IQ3_S / IQ3_XXS / Q2_0 row), up to 256 pairs.
 inline bool direct_takes(const MatvecParams& p) {
   const int runs = p.cols / 32;
@@ -906,6 +1059,7 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
         if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }
+      if (!glu && one && odd_takes(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
       if (direct_takes(p)) {
         return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
                    : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);
