@@ -331,6 +331,15 @@ __device__ __forceinline__ void arrived(uint32_t (&v)[32]) {
                  "+v"(v[i + 6]), "+v"(v[i + 7]));
 }
 
+// These 32 registers hold nothing yet: an empty definition, so the compiler does not materialize a value for
+// them on this path (it would otherwise zero all 32 where the other path loads them).
+__device__ __forceinline__ void unset(uint32_t (&v)[32]) {
+#pragma unroll
+  for (int i = 0; i < 32; i += 8)
+    asm volatile("" : "=v"(v[i]), "=v"(v[i + 1]), "=v"(v[i + 2]), "=v"(v[i + 3]), "=v"(v[i + 4]), "=v"(v[i + 5]),
+                 "=v"(v[i + 6]), "=v"(v[i + 7]));
+}
+
 // the lowest pair left in the four masks, taken out; -1 when none is
 __device__ __forceinline__ int take_lowest(uint64_t& m) {
   const int b = __ffsll((unsigned long long)m) - 1;
@@ -600,6 +609,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
     const u32x4* src = reinterpret_cast<const u32x4*>(p.x);
 #pragma unroll
     for (int k = 0; k < 2; ++k) xv[k] = src[min(tid + k * kThreads, p.cols / 8 - 1)];
+    unset(x[0]);  // read from LDS after the barrier
   } else if constexpr (!GLU) {
     fast_load_x<false>(p, q0, run_of<KIND>(jp, 0), x[0]);
     fast_load_x<false>(p, q0, run_of<KIND>(jp, 1), x[0] + 16);
