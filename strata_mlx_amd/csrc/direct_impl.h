@@ -109,6 +109,43 @@ struct DirectTables {
   u32x2 q2[FastTraits<KIND>::q2 > 0 ? FastTraits<KIND>::q2 : 1];  // a Q2_0 code byte: four (c - 1)
 };
 
+// (byte K of v) * 8 and (16-bit word K of v) * 8 in one instruction each: a shift whose operand is a byte / word
+// select (SDWA). The compiler selects these forms itself for the upper bytes and word, and two instructions
+// (shift, mask) for the lowest. `three` holds 3.
+template <int K>
+__device__ __forceinline__ uint32_t byte_x8(uint32_t v, uint32_t three) {
+  uint32_t r;
+  if constexpr (K == 0)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r) : "v"(three), "v"(v));
+  else if constexpr (K == 1)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(r) : "v"(three), "v"(v));
+  else if constexpr (K == 2)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(r) : "v"(three), "v"(v));
+  else
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(r) : "v"(three), "v"(v));
+  return r;
+}
+template <int K>
+__device__ __forceinline__ uint32_t word_x8(uint32_t v, uint32_t three) {
+  uint32_t r;
+  if constexpr (K == 0)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+        : "=v"(r) : "v"(three), "v"(v));
+  else
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+        : "=v"(r) : "v"(three), "v"(v));
+  return r;
+}
+
+// 8 bytes of LDS at byte offset off from table t
+__device__ __forceinline__ u32x2 lds_entry(const u32x2* t, uint32_t off) {
+  return *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(t) + off);
+}
+
 // run h (0, 1) of a pair: 16 packed float16 pairs of integers, and the run's scale
 template <int KIND>
 __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, int j, uint32_t* w,
@@ -123,12 +160,20 @@ __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, int 
     const uint32_t hb1 = (__builtin_amdgcn_ubfe(qh, 4, 4) * 0x204081u) & 0x01010101u;
     const uint32_t i01 = __builtin_amdgcn_perm(hb0, qs0, 0x05010400u), i23 = __builtin_amdgcn_perm(hb0, qs0, 0x07030602u);
     const uint32_t i45 = __builtin_amdgcn_perm(hb1, qs1, 0x05010400u), i67 = __builtin_amdgcn_perm(hb1, qs1, 0x07030602u);
-    const uint32_t ix[8] = {i01 & 0xffff, i01 >> 16, i23 & 0xffff, i23 >> 16,
-                            i45 & 0xffff, i45 >> 16, i67 & 0xffff, i67 >> 16};
+    const uint32_t three = 3;
+    // byte offsets of the codebook entries (index * 8) and of the sign masks (nibble * 8): the sign nibbles split
+    // into the bytes of two words (groups 0, 2, 4, 6 and 1, 3, 5, 7), each then one byte select
+    const uint32_t ga[8] = {word_x8<0>(i01, three), word_x8<1>(i01, three), word_x8<0>(i23, three),
+                            word_x8<1>(i23, three), word_x8<0>(i45, three), word_x8<1>(i45, three),
+                            word_x8<0>(i67, three), word_x8<1>(i67, three)};
+    const uint32_t se = sg & 0x0F0F0F0Fu, so = (sg >> 4) & 0x0F0F0F0Fu;
+    const uint32_t sa[8] = {byte_x8<0>(se, three), byte_x8<0>(so, three), byte_x8<1>(se, three),
+                            byte_x8<1>(so, three), byte_x8<2>(se, three), byte_x8<2>(so, three),
+                            byte_x8<3>(se, three), byte_x8<3>(so, three)};
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
-      const u32x2 g = t.grid[ix[l]];
-      const u32x2 m = t.sign4[(sg >> (4 * l)) & 15];
+      const u32x2 g = lds_entry(t.grid, ga[l]);
+      const u32x2 m = lds_entry(t.sign4, sa[l]);
       w[2 * l] = g[0] ^ m[0];
       w[2 * l + 1] = g[1] ^ m[1];
     }
