@@ -917,8 +917,8 @@ int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
 // idle. Here 8 lanes take a row and lane m takes its run pairs m, m + 8, ... (S steps of eight consecutive run
 // pairs, every lane busy), so a wave holds 8 rows, and a row's sum meets over 8 lanes by three DPP steps. The
 // lane's activations differ from step to step: the pair's token sits in LDS (one copy for the workgroup, whose
-// waves all multiply the same pair) and each step reads its 128 bytes. Routed pairs or a matrix a pair, one token
-// a pass.
+// waves all multiply the same pair) and each step reads its 128 bytes. Routed pairs, a matrix a pair, or a window
+// (its tokens one a pass, listed rows as in direct_decode_kernel), one token a pass.
 template <int KIND, int S>
 __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(MatvecParams p) {
   constexpr int kPairs = 8 * S;     // run pairs of a row
@@ -932,11 +932,17 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
   const bool in_range = tile < p.ntiles;
   const int pair = blockIdx.z, z0 = blockIdx.y;
   const int r0 = (in_range ? tile : 0) * 8;
-  const int row = min(r0 + sub, p.rows - 1);
-  const bool routed = p.mode == MODE_EXPERT;
+  const bool routed = p.mode == MODE_EXPERT, dense = p.mode == MODE_DENSE;
+  const int rl = min(r0 + sub, p.rows - 1);  // the lane's output row
+  uint32_t row = (uint32_t)rl;               // the matrix row it reads: a listed row's id (past the matrix: row 0)
+  if (dense && p.row_ids != nullptr) {
+    const uint32_t id = p.row_ids[rl];
+    row = id < (uint32_t)p.src_rows ? id : 0u;
+  }
   const uint32_t expert = routed ? p.idx[pair] : 0u;
   const bool bad = routed && expert >= (uint64_t)p.experts;
-  const uint8_t* m0 = routed ? p.blocks[z0] + (int64_t)(bad ? 0u : expert) * p.mat_bytes : p.ptrs[pair];
+  const uint8_t* m0 = routed ? p.blocks[z0] + (int64_t)(bad ? 0u : expert) * p.mat_bytes
+                             : dense ? p.blocks[z0] : p.ptrs[pair];
 
   // loads in the order they are waited for: the tables' constants and the pairs' ids, the token, the rows
   TableFetch<KIND> tf;
@@ -948,13 +954,14 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
   }
   const bool one_x = routed && p.share == p.pairs;  // every pair the same token: one pass writes them all
   u32x4 xv[(kPieces + kThreads - 1) / kThreads];
-  const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(p.x) + (int64_t)(pair / p.share) * p.cols);
+  const int x0 = dense ? 0 : pair / p.share;  // the first pass's token
+  const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(p.x) + (int64_t)x0 * p.cols);
 #pragma unroll
   for (int k = 0; k * kThreads < kPieces; ++k) xv[k] = src[min(tid + k * kThreads, kPieces - 1)];
   RunPair<KIND> f[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    load_fields<KIND>(m0, (uint32_t)row * (uint32_t)p.row_bytes, lane_offsets<KIND>(8 * s + m), f[s]);
+    load_fields<KIND>(m0, row * (uint32_t)p.row_bytes, lane_offsets<KIND>(8 * s + m), f[s]);
     asm volatile("" ::: "memory");  // the steps' loads go out in step order: step 0 is decoded first
   }
   asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(tf.g[0]), "+v"(tf.g[1])::"memory");
@@ -987,10 +994,12 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
     return;
   }
   for (int pass = 0;; ++pass) {
-    const int q = take_member(mb[0], mb[1], mb[2], mb[3]);  // this pass's pair (the first: this one)
+    // this pass's output row block: a window's token, or a pair naming the expert (the first: this one)
+    const int q = dense ? (pass < p.tokens ? pass : -1) : take_member(mb[0], mb[1], mb[2], mb[3]);
     if (q < 0) break;
-    if (pass > 0) {  // the next pair's token into LDS, once every wave is done with the last one
-      const u32x4* sq = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(p.x) + (int64_t)(q / p.share) * p.cols);
+    if (pass > 0) {  // the next token into LDS, once every wave is done with the last one
+      const int xq = dense ? q : q / p.share;
+      const u32x4* sq = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(p.x) + (int64_t)xq * p.cols);
 #pragma unroll
       for (int k = 0; k * kThreads < kPieces; ++k) xv[k] = sq[min(tid + k * kThreads, kPieces - 1)];
       __syncthreads();
@@ -1022,6 +1031,7 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
     acc += lanes_apart(acc, 2);
     acc += lanes_apart(acc, 4);
     if (m == 0 && in_range && r0 + sub < p.rows) {  // this pass's pair, or (one token) every pair naming the expert
+      if (dense && p.row_ids != nullptr && p.row_ids[rl] >= (uint32_t)p.src_rows) acc = __builtin_nanf("");  // past it
       const f16 v = from_f32<f16>(acc);
       f16* out = reinterpret_cast<f16*>(p.out[z0]) + r0 + sub;
       out[(int64_t)q * p.rows] = v;
@@ -1037,32 +1047,45 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
 // direct_odd_kernel.
 template <int KIND>
 int launch_direct_odd(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
-  const int pairs = p.cols / 64;
-  if (grid_y > kDMaxGridY || grid_z > kDMaxGridY || (int64_t)p.rows * p.row_bytes >= ((int64_t)1 << 32))
+  if constexpr (KIND == K_Q4_K || KIND == K_Q8_0) {
     return STRATA_ERR_SHAPE;
-  p.nz = grid_z;
-  p.ntiles = (p.rows + 7) / 8;
-  p.items = p.ntiles;
-  const dim3 grid((p.ntiles + kWaves - 1) / kWaves, grid_z, grid_y);
-  if (pairs == 24) {
-    hipLaunchKernelGGL((direct_odd_kernel<KIND, 3>), grid, dim3(kThreads), 0, stream, p);
-  } else if (pairs == 40) {
-    hipLaunchKernelGGL((direct_odd_kernel<KIND, 5>), grid, dim3(kThreads), 0, stream, p);
   } else {
-    return STRATA_ERR_SHAPE;
+    const int pairs = p.cols / 64;
+    if (grid_y > kDMaxGridY || grid_z > kDMaxGridY ||
+        (int64_t)std::max(p.rows, p.src_rows) * p.row_bytes >= ((int64_t)1 << 32))
+      return STRATA_ERR_SHAPE;
+    p.nz = grid_z;
+    p.ntiles = (p.rows + 7) / 8;
+    p.items = p.ntiles;
+    const dim3 grid((p.ntiles + kWaves - 1) / kWaves, grid_z, grid_y);
+    if (pairs == 24) {
+      hipLaunchKernelGGL((direct_odd_kernel<KIND, 3>), grid, dim3(kThreads), 0, stream, p);
+    } else if (pairs == 40) {
+      hipLaunchKernelGGL((direct_odd_kernel<KIND, 5>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      return STRATA_ERR_SHAPE;
+    }
+    STRATA_CHECK_LAUNCH();
+    return STRATA_OK;
   }
-  STRATA_CHECK_LAUNCH();
-  return STRATA_OK;
 }
 
-inline bool odd_takes(const MatvecParams& p) {
+// Whether direct_odd_kernel takes the call: rows of 24 / 40 run pairs, one token a pass. The codebook types at
+// both widths; Q3_K and Q6_K at 40 run pairs only (at 24, as fast as direct_decode_kernel's 32-lane rows); not
+// Q8_0 (its five-step form holds three waves a SIMD and is slower) nor Q4_K (with its run sums of x it spills).
+template <int KIND>
+bool odd_takes(const MatvecParams& p) {
+  if constexpr (KIND == K_Q4_K || KIND == K_Q8_0) return false;
+  if (DirectKind<KIND>::linear && p.cols != 40 * 64) return false;
   static const bool on = [] {  // STRATA_ODD_ROWS=0: such rows take direct_decode_kernel (to compare)
     const char* e = getenv("STRATA_ODD_ROWS");
     return !(e && e[0] == '0');
   }();
-  return on && p.cols % 64 == 0 && (p.cols / 64 == 24 || p.cols / 64 == 40) &&
-         (p.mode == MODE_EXPERT || p.mode == MODE_PTRS) && p.pairs <= kDMaxPairs && p.row_ids == nullptr &&
-         p.glu_out == nullptr;
+  // listed rows (dense): when the matrix's byte offsets fit 32 bits
+  const bool ids_ok = p.row_ids == nullptr ||
+                      (p.mode == MODE_DENSE && (int64_t)p.src_rows * p.row_bytes < ((int64_t)1 << 32));
+  return on && p.cols % 64 == 0 && (p.cols / 64 == 24 || p.cols / 64 == 40) && ids_ok &&
+         (p.mode == MODE_DENSE || p.pairs <= kDMaxPairs) && p.glu_out == nullptr;
 }
 
 // Rows of 64 to 4096 weights in run pairs (every IQ3_S / IQ3_XXS / Q2_0 row), up to 256 pairs.
@@ -1101,6 +1124,8 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
         if (glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }
+      // one token a pass either way: rows of 24 / 40 run pairs on 8 lanes a row
+      if (!glu && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
       return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
                  : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);
     }
@@ -1114,7 +1139,7 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
         if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }
-      if (!glu && one && odd_takes(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
+      if (!glu && one && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
       if (direct_takes(p)) {
         return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
                    : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);

@@ -1,9 +1,9 @@
-"""Rows of 24 and 40 run pairs (1536 and 2560 inputs: the down projection, 2560-wide experts) at one token a pass,
+"""Rows of 24 and 40 run pairs (1536 and 2560 inputs: the down projection, 2560-wide layers) at one token a pass,
 the kernel that gives a row 8 lanes: against the float64 product of the oracle's weights (test_blocks.py:65:
 2e-3 relative for float16), with an expert named by several pairs (a pass a pair, the token reloaded), every
 pair on one token (one pass written to each pair naming the expert), row counts that are not a multiple of 8,
-a pair alone against the same pair among others (the same bits), and a matrix a pair against the stack
-(matvec_separate, blocks.py:331: the same bits)."""
+a pair alone against the same pair among others (the same bits), a matrix a pair against the stack
+(matvec_separate, blocks.py:331: the same bits), windows of one and three tokens, and listed rows."""
 
 import numpy as np
 import pytest
@@ -78,3 +78,39 @@ def test_a_matrix_a_pair_gives_the_bits_of_the_stack_at_1536(gpu, kind):
     got = B.matvec_separate(experts, kind, rows, cols, x, 2)
     want = layer(x.reshape(2, 1, 1, cols), dev(np.array([[2, 0], [1, 1]]), gpu)).reshape(4, rows)
     assert torch.equal(got, want)
+
+
+WINDOW_KINDS = ["IQ3_S", "IQ3_XXS", "Q2_0", "Q3_K", "Q6_K", "Q8_0"]
+
+
+@pytest.mark.parametrize("kind", WINDOW_KINDS)
+@pytest.mark.parametrize("cols", [1536, 2560])
+@pytest.mark.parametrize("tokens", [1, 3])
+def test_a_window_of_odd_rows_is_the_product(gpu, kind, cols, tokens):
+    """window_matvec (blocks.py:383-394) on rows of 24 / 40 run pairs: test_dense.py:49's 4e-3 of the largest
+    output for float16."""
+    rng = np.random.default_rng(cols + tokens)
+    rows = 53
+    data, w = stack(kind, rng, 1, rows, cols)
+    x = torch.randn((tokens, cols), generator=torch.Generator().manual_seed(tokens)).half()
+    got = B.window_matvec(dev(data, gpu), kind, rows, cols, x.to(gpu)).float().cpu().numpy()
+    want = x.double().numpy() @ w[0].T
+    assert got.shape == (tokens, rows)
+    assert np.abs(got - want).max() <= 4e-3 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("kind", ["Q3_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("cols", [1536, 2560])
+def test_listed_rows_of_odd_rows_have_the_layers_bits(gpu, kind, cols):
+    """rows.py:30-42: rows by id give the full layer's outputs bit for bit; an id past the layer gives NaN."""
+    rng = np.random.default_rng(3)
+    rows = 300
+    data, _ = stack(kind, rng, 1, rows, cols)
+    blocks = dev(data, gpu)
+    x = torch.randn((1, cols), generator=torch.Generator().manual_seed(2)).half().to(gpu)
+    full = B.window_matvec(blocks, kind, rows, cols, x)
+    ids = torch.tensor([5, 299, 0, 17, 17, 250, 3, 101, 77, 128, 64], dtype=torch.int32, device=gpu)
+    got = B.window_matvec(blocks, kind, rows, cols, x, row_ids=ids)
+    assert torch.equal(got, full[:, ids.long()])
+    bad = B.window_matvec(blocks, kind, rows, cols, x, row_ids=torch.tensor([1, 300], dtype=torch.int32, device=gpu))
+    assert torch.isfinite(bad[0, 0]) and torch.isnan(bad[0, 1])
