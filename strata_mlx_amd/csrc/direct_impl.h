@@ -1139,7 +1139,10 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
         if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }
-      if (!glu && one && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
+      // up to 64 pairs (8 tokens at top-8) one token a pass on the 8-lane rows beats two a pass on 32-lane rows
+      // (four tokens: 2283 against 2047 GB/s); with more, pairs share experts often enough that the second
+      // token a pass is worth more than the idle lanes
+      if (!glu && (one || p.pairs <= 64) && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
       if (direct_takes(p)) {
         return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
                    : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);
