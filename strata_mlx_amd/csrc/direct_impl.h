@@ -81,10 +81,19 @@ struct RunPair<K_Q3_K> {
   uint16_t d;
 };
 
+template <>
+struct RunPair<K_IQ4_XS> {
+  u32x4 qs[2];   // the lane's two runs' 16 code bytes each (weights 0-15 in the low nibbles, 16-31 in the high)
+  uint32_t dh;   // d | scales_h << 16
+  uint32_t sl;   // the four scales_l bytes (run 2k's low four scale bits in byte k's low nibble)
+};
+
 template <int KIND>
 struct DirectKind {
-  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K;
+  static constexpr bool linear =
+      KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K || KIND == K_IQ4_XS;
   static constexpr bool any = FastTraits<KIND>::supported || linear;
+  static constexpr int pair_codes = KIND == K_IQ4_XS ? 256 : 0;  // a table of two codebook values a byte
 };
 
 // A load from global memory at any alignment (gfx950 serves 2-byte aligned dwordx2/x4 loads as they are).
@@ -107,13 +116,15 @@ struct DirectTables {
   u32x2 grid[FastTraits<KIND>::grid > 0 ? FastTraits<KIND>::grid : 1];
   u32x2 sign4[16];
   u32x2 q2[FastTraits<KIND>::q2 > 0 ? FastTraits<KIND>::q2 : 1];  // a Q2_0 code byte: four (c - 1)
+  // IQ4_XS: byte lo | hi << 4 -> the float16 pair (kvalues[lo], kvalues[hi])
+  uint32_t kv2[DirectKind<KIND>::pair_codes > 0 ? DirectKind<KIND>::pair_codes : 1];
 };
 
-// (byte K of v) * 8 and (16-bit word K of v) * 8 in one instruction each: a shift whose operand is a byte / word
-// select (SDWA). The compiler selects these forms itself for the upper bytes and word, and two instructions
-// (shift, mask) for the lowest. `three` holds 3.
+// (byte K of v) << sh and (16-bit word K of v) << sh in one instruction each: a shift whose operand is a byte /
+// word select (SDWA). The compiler selects these forms itself for the upper bytes and word, and two
+// instructions (shift, mask) for the lowest. sh is a register (3: table entries of 8 bytes, 2: of 4).
 template <int K>
-__device__ __forceinline__ uint32_t byte_x8(uint32_t v, uint32_t three) {
+__device__ __forceinline__ uint32_t byte_shl(uint32_t v, uint32_t three) {
   uint32_t r;
   if constexpr (K == 0)
     asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
@@ -130,7 +141,7 @@ __device__ __forceinline__ uint32_t byte_x8(uint32_t v, uint32_t three) {
   return r;
 }
 template <int K>
-__device__ __forceinline__ uint32_t word_x8(uint32_t v, uint32_t three) {
+__device__ __forceinline__ uint32_t word_shl(uint32_t v, uint32_t three) {
   uint32_t r;
   if constexpr (K == 0)
     asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
@@ -163,13 +174,13 @@ __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, int 
     const uint32_t three = 3;
     // byte offsets of the codebook entries (index * 8) and of the sign masks (nibble * 8): the sign nibbles split
     // into the bytes of two words (groups 0, 2, 4, 6 and 1, 3, 5, 7), each then one byte select
-    const uint32_t ga[8] = {word_x8<0>(i01, three), word_x8<1>(i01, three), word_x8<0>(i23, three),
-                            word_x8<1>(i23, three), word_x8<0>(i45, three), word_x8<1>(i45, three),
-                            word_x8<0>(i67, three), word_x8<1>(i67, three)};
+    const uint32_t ga[8] = {word_shl<0>(i01, three), word_shl<1>(i01, three), word_shl<0>(i23, three),
+                            word_shl<1>(i23, three), word_shl<0>(i45, three), word_shl<1>(i45, three),
+                            word_shl<0>(i67, three), word_shl<1>(i67, three)};
     const uint32_t se = sg & 0x0F0F0F0Fu, so = (sg >> 4) & 0x0F0F0F0Fu;
-    const uint32_t sa[8] = {byte_x8<0>(se, three), byte_x8<0>(so, three), byte_x8<1>(se, three),
-                            byte_x8<1>(so, three), byte_x8<2>(se, three), byte_x8<2>(so, three),
-                            byte_x8<3>(se, three), byte_x8<3>(so, three)};
+    const uint32_t sa[8] = {byte_shl<0>(se, three), byte_shl<0>(so, three), byte_shl<1>(se, three),
+                            byte_shl<1>(so, three), byte_shl<2>(se, three), byte_shl<2>(so, three),
+                            byte_shl<3>(se, three), byte_shl<3>(so, three)};
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       const u32x2 g = lds_entry(t.grid, ga[l]);
@@ -267,6 +278,24 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
       sc[e] = d * (float)((int)v - 32);
     }
     return RunScale{sc[0], sc[1]};
+  } else if constexpr (KIND == K_IQ4_XS) {  // w = d * (ls - 32) * kvalues[code], strata_mlx/blocks.py:78-88
+    // four code bytes b0..b3: their low nibbles are weights 4k .. 4k + 3, their high ones 16 + 4k ..; OR-ing the
+    // nibbles with themselves four bits down puts the pairs (b0, b1) and (b2, b3) in bytes 0 and 2, the index
+    // of the pair table
+    const uint32_t two = 2;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t q = f.qs[h][k];
+      const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+      const uint32_t tl = lo | (lo >> 4), th = hi | (hi >> 4);
+      w[2 * k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<0>(tl, two));
+      w[2 * k + 1] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<2>(tl, two));
+      w[8 + 2 * k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<0>(th, two));
+      w[9 + 2 * k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<2>(th, two));
+    }
+    const int jj = j & 3, ib = 2 * jj + h;  // the block's run
+    const uint32_t ls = ((f.sl >> (8 * jj + 4 * h)) & 15) | (((f.dh >> (16 + 2 * ib)) & 3) << 4);
+    return RunScale{half_bits(f.dh & 0xffff) * (float)((int)ls - 32), 0.0f};
   } else {
     return RunScale{decode_pair<KIND>(f, h, j, w, t), 0.0f};
   }
@@ -331,6 +360,10 @@ __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableF
     const u32x4 m = sign_masks((uint32_t)tid);
     t.sign4[tid] = u32x2{m[0], m[1]};
   }
+  if constexpr (DirectKind<KIND>::pair_codes > 0) {
+    for (int i = tid; i < 256; i += NT)
+      t.kv2[i] = pack_h2((float)kStrataKvaluesIq4nl[i & 15], (float)kStrataKvaluesIq4nl[i >> 4]);
+  }
   if constexpr (FastTraits<KIND>::q2 > 0) {
     for (int i = tid; i < 256; i += NT)
       t.q2[i] = u32x2{pack_h2((float)(i & 3) - 1.0f, (float)((i >> 2) & 3) - 1.0f),
@@ -355,6 +388,9 @@ __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
     return;
   } else if constexpr (KIND == K_Q3_K) {
     asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.hm[0]), "+v"(f.hm[1]), "+v"(f.lo), "+v"(f.hi), "+v"(f.d));
+    return;
+  } else if constexpr (KIND == K_IQ4_XS) {
+    asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.dh), "+v"(f.sl));
     return;
   } else {
 #pragma unroll
@@ -434,6 +470,11 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.a = b;
     o.b = b + 96 + 4 * (jj & 1);
     o.c = b + 104;
+  } else if constexpr (KIND == K_IQ4_XS) {  // d @0, scales_h @2, scales_l[4] @4, qs[128] @8 (run ib @8 + 16 ib)
+    const uint32_t b = (j >> 2) * 136, jj = j & 3;
+    o.d = b;
+    o.a = b + 4;
+    o.qs = b + 8 + 32 * jj;
   } else if constexpr (KIND == K_Q6_K) {  // ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208
     const uint32_t b = (j >> 2) * 210, hh = (j >> 1) & 1, r0 = j & 1;
     o.d = b + 208;
@@ -506,6 +547,12 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
     f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
     f.hm[0] = load_at<u32x4>(row, lo + o.a);
     f.hm[1] = load_at<u32x4>(row, lo + o.a + 16);
+    return;
+  } else if constexpr (KIND == K_IQ4_XS) {
+    f.dh = load_at<uint32_t>(row, lo + o.d);
+    f.sl = load_at<uint32_t>(row, lo + o.a);
+    f.qs[0] = load_at<u32x4>(row, lo + o.qs);
+    f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
     return;
   } else if constexpr (KIND == K_Q6_K) {
     f.d = load_at<uint16_t>(row, lo + o.d);
