@@ -80,7 +80,7 @@ def test_a_matrix_a_pair_gives_the_bits_of_the_stack_at_1536(gpu, kind):
     assert torch.equal(got, want)
 
 
-WINDOW_KINDS = ["IQ3_S", "IQ3_XXS", "Q2_0", "Q3_K", "Q6_K", "Q8_0"]
+WINDOW_KINDS = ["IQ3_S", "IQ3_XXS", "Q2_0", "Q3_K", "Q6_K", "Q8_0", "IQ4_XS"]
 
 
 @pytest.mark.parametrize("kind", WINDOW_KINDS)
@@ -99,7 +99,7 @@ def test_a_window_of_odd_rows_is_the_product(gpu, kind, cols, tokens):
     assert np.abs(got - want).max() <= 4e-3 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("kind", ["Q3_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("kind", ["Q3_K", "Q6_K", "Q8_0", "IQ4_XS"])
 @pytest.mark.parametrize("cols", [1536, 2560])
 def test_listed_rows_of_odd_rows_have_the_layers_bits(gpu, kind, cols):
     """rows.py:30-42: rows by id give the full layer's outputs bit for bit; an id past the layer gives NaN."""
