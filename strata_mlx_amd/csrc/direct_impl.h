@@ -88,12 +88,19 @@ struct RunPair<K_IQ4_XS> {
   uint32_t sl;   // the four scales_l bytes (run 2k's low four scale bits in byte k's low nibble)
 };
 
+template <>
+struct RunPair<K_IQ4_NL> {
+  u32x4 qs[2];     // the lane's two blocks' 16 code bytes each
+  uint16_t d[2];
+};
+
 template <int KIND>
 struct DirectKind {
-  static constexpr bool linear =
-      KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K || KIND == K_IQ4_XS;
+  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K ||
+                                 KIND == K_IQ4_XS || KIND == K_IQ4_NL;
   static constexpr bool any = FastTraits<KIND>::supported || linear;
-  static constexpr int pair_codes = KIND == K_IQ4_XS ? 256 : 0;  // a table of two codebook values a byte
+  // a table of two codebook values a byte (the 16-entry IQ4 codebook)
+  static constexpr int pair_codes = KIND == K_IQ4_XS || KIND == K_IQ4_NL ? 256 : 0;
 };
 
 // A load from global memory at any alignment (gfx950 serves 2-byte aligned dwordx2/x4 loads as they are).
@@ -116,7 +123,7 @@ struct DirectTables {
   u32x2 grid[FastTraits<KIND>::grid > 0 ? FastTraits<KIND>::grid : 1];
   u32x2 sign4[16];
   u32x2 q2[FastTraits<KIND>::q2 > 0 ? FastTraits<KIND>::q2 : 1];  // a Q2_0 code byte: four (c - 1)
-  // IQ4_XS: byte lo | hi << 4 -> the float16 pair (kvalues[lo], kvalues[hi])
+  // IQ4_XS / IQ4_NL: byte lo | hi << 4 -> the float16 pair (kvalues[lo], kvalues[hi])
   uint32_t kv2[DirectKind<KIND>::pair_codes > 0 ? DirectKind<KIND>::pair_codes : 1];
 };
 
@@ -231,6 +238,25 @@ struct RunScale {
   float a, b;
 };
 
+// A run's 16 code bytes of the IQ4 codebook -> its 32 weights as 16 float16 pairs, from the pair table kv2.
+// Four code bytes b0..b3: their low nibbles are weights 4k .. 4k + 3, their high ones 16 + 4k ..; OR-ing the
+// nibbles with themselves four bits down puts the pairs (b0, b1) and (b2, b3) in bytes 0 and 2: the index of
+// the pair table, two weights a lookup.
+__device__ __forceinline__ void pair_codes_run(const u32x4& qs, uint32_t* w, const uint32_t* kv2) {
+  const uint32_t two = 2;
+  const char* base = reinterpret_cast<const char*>(kv2);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t q = qs[k];
+    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+    const uint32_t tl = lo | (lo >> 4), th = hi | (hi >> 4);
+    w[2 * k] = *reinterpret_cast<const uint32_t*>(base + byte_shl<0>(tl, two));
+    w[2 * k + 1] = *reinterpret_cast<const uint32_t*>(base + byte_shl<2>(tl, two));
+    w[8 + 2 * k] = *reinterpret_cast<const uint32_t*>(base + byte_shl<0>(th, two));
+    w[9 + 2 * k] = *reinterpret_cast<const uint32_t*>(base + byte_shl<2>(th, two));
+  }
+}
+
 // Run h (0, 1) of lane run pair j: 16 packed float16 pairs of integers into w, and its scales.
 template <int KIND>
 __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, int j, uint32_t* w,
@@ -278,21 +304,11 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
       sc[e] = d * (float)((int)v - 32);
     }
     return RunScale{sc[0], sc[1]};
+  } else if constexpr (KIND == K_IQ4_NL) {  // w = d * kvalues[code], strata_mlx/blocks.py:69-77
+    pair_codes_run(f.qs[h], w, t.kv2);
+    return RunScale{half_bits(f.d[h]), 0.0f};
   } else if constexpr (KIND == K_IQ4_XS) {  // w = d * (ls - 32) * kvalues[code], strata_mlx/blocks.py:78-88
-    // four code bytes b0..b3: their low nibbles are weights 4k .. 4k + 3, their high ones 16 + 4k ..; OR-ing the
-    // nibbles with themselves four bits down puts the pairs (b0, b1) and (b2, b3) in bytes 0 and 2, the index
-    // of the pair table
-    const uint32_t two = 2;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t q = f.qs[h][k];
-      const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
-      const uint32_t tl = lo | (lo >> 4), th = hi | (hi >> 4);
-      w[2 * k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<0>(tl, two));
-      w[2 * k + 1] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<2>(tl, two));
-      w[8 + 2 * k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<0>(th, two));
-      w[9 + 2 * k] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(t.kv2) + byte_shl<2>(th, two));
-    }
+    pair_codes_run(f.qs[h], w, t.kv2);
     const int jj = j & 3, ib = 2 * jj + h;  // the block's run
     const uint32_t ls = ((f.sl >> (8 * jj + 4 * h)) & 15) | (((f.dh >> (16 + 2 * ib)) & 3) << 4);
     return RunScale{half_bits(f.dh & 0xffff) * (float)((int)ls - 32), 0.0f};
@@ -392,6 +408,9 @@ __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
   } else if constexpr (KIND == K_IQ4_XS) {
     asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.dh), "+v"(f.sl));
     return;
+  } else if constexpr (KIND == K_IQ4_NL) {
+    asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.d[0]), "+v"(f.d[1]));
+    return;
   } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(f.qs[i]));
@@ -470,6 +489,9 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.a = b;
     o.b = b + 96 + 4 * (jj & 1);
     o.c = b + 104;
+  } else if constexpr (KIND == K_IQ4_NL) {  // two blocks of 18: d @0, qs[16] @2
+    o.d = j * 36;
+    o.qs = j * 36 + 2;
   } else if constexpr (KIND == K_IQ4_XS) {  // d @0, scales_h @2, scales_l[4] @4, qs[128] @8 (run ib @8 + 16 ib)
     const uint32_t b = (j >> 2) * 136, jj = j & 3;
     o.d = b;
@@ -547,6 +569,12 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
     f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
     f.hm[0] = load_at<u32x4>(row, lo + o.a);
     f.hm[1] = load_at<u32x4>(row, lo + o.a + 16);
+    return;
+  } else if constexpr (KIND == K_IQ4_NL) {
+    f.d[0] = load_at<uint16_t>(row, lo + o.d);
+    f.qs[0] = load_at<u32x4>(row, lo + o.qs);
+    f.d[1] = load_at<uint16_t>(row, lo + o.d + 18);
+    f.qs[1] = load_at<u32x4>(row, lo + o.qs + 18);
     return;
   } else if constexpr (KIND == K_IQ4_XS) {
     f.dh = load_at<uint32_t>(row, lo + o.d);
