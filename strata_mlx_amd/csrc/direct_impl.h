@@ -1207,17 +1207,17 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
   }
   if constexpr (FastTraits<KIND>::supported) {
     if (x_dtype == DT_F16 && out_dtype == DT_F16 && p.row_ids == nullptr) {
+      // one token a pass (four waves a SIMD) up to 64 routed pairs: most experts are named once, and the second
+      // token a pass (three waves a SIMD) pays only where they are not (four tokens: 2458 against 2343 GB/s)
       const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
                                                                      : (glu ? p.pairs <= 16
-                                                                            : p.pairs <= p.share || p.pairs <= 8));
+                                                                            : p.pairs <= p.share || p.pairs <= 64));
       if (p.glu_out != nullptr) {
         if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }
-      // up to 64 pairs (8 tokens at top-8) one token a pass on the 8-lane rows beats two a pass on 32-lane rows
-      // (four tokens: 2283 against 2047 GB/s); with more, pairs share experts often enough that the second
-      // token a pass is worth more than the idle lanes
-      if (!glu && (one || p.pairs <= 64) && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
+      // the same for the 8-lane rows against two tokens a pass on 32-lane rows (four tokens: 2283 against 2047)
+      if (!glu && one && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
       if (direct_takes(p)) {
         return glu ? launch_direct<KIND, true, false>(p, one, grid_y, grid_z, s)
                    : launch_direct<KIND, false, false>(p, one, grid_y, grid_z, s);
