@@ -1,20 +1,23 @@
 // The decode matvec for float16 activations, rows read straight into registers (IQ3_S, IQ3_XXS, Q2_0 with
-// their codebooks in LDS; Q4_K, Q6_K, Q8_0 decoded by byte arithmetic alone).
+// their codebooks in LDS; Q3_K, Q4_K, Q6_K, Q8_0 decoded by byte arithmetic; IQ4_XS, IQ4_NL through an LDS table
+// of codebook pairs).
 //
 // A decode call moves tens of megabytes in a few microseconds, so what matters is that every byte is requested
 // at once: a wave's loads go out as soon as it knows its expert, before anything else it does. Nothing is staged
-// in LDS except the codebooks. A lane takes two consecutive runs of one block (64 weights) of a row and loads
-// exactly their fields into registers (IQ3_S: the 16 index bytes, the two high-bit bytes, the eight sign bytes,
-// the scale byte and d: five loads at 2-byte alignment, which gfx950 serves as they are). A row is L lanes (its
-// run pairs rounded up to a power of two: 64 for 4096 inputs, 32 for 1536), 64 / L rows side by side; a wave
-// takes RU such row steps of one matrix (a "unit"), all loaded before the first is decoded. Codebook entries
-// come from LDS as float16 and sign masks (as in fast_impl.h), products from v_dot2_f32_f16 against the
-// activations packed in registers, and a row's partial sums meet across its lanes by shuffles.
+// in LDS except the codebooks and a token the workgroup shares. A lane takes two consecutive runs of one block
+// (64 weights) of a row and loads exactly their fields into registers (IQ3_S: the 16 index bytes, the two
+// high-bit bytes, the eight sign bytes, the scale bytes and d: five loads at 2-byte alignment, which gfx950 serves
+// as they are). A row is L lanes (its run pairs rounded up to a power of two: 64 for 4096 inputs, 32 for 1536),
+// 64 / L rows side by side; a wave takes RU such row steps of one matrix (a "unit"), all loaded before the first
+// is decoded, and decodes each step as soon as that step's own loads are in. Codebook entries come from LDS as
+// float16 and sign masks, products from v_dot2_f32_f16 against the activations packed in registers, and a row's
+// partial sums meet across its lanes by DPP and row swaps. Rows of 24 or 40 run pairs, which fill such rows
+// badly, take direct_odd_kernel: 8 lanes a row, every lane busy.
 //
-// The routed form gives a wave (pair, stack, rows). A pair whose expert an earlier pair names leaves its rows to
-// that pair's waves, which multiply them by every pair naming the expert (ballots over the pairs' ids, TT pairs
-// a pass). When every pair multiplies the same token (one token's gate/up), the rows are multiplied once and the
-// sum is written for every pair naming the expert.
+// The routed form gives a wave (pair, stack, rows), from a grid of (units, stacks, pairs). A pair whose expert
+// an earlier pair names leaves its rows to that pair's waves, which multiply them by every pair naming the expert
+// (ballots over the pairs' ids, TT pairs a pass). When every pair multiplies the same token (one token's
+// gate/up), the rows are multiplied once and the sum is written for every pair naming the expert.
 //
 // Paired mode (gate and up of one call): a unit's row steps alternate between the two stacks, the same rows of
 // each, so the lane that ends with row r's gate sum also has its up sum, and writes silu(gate) * up as mlx-lm
