@@ -347,11 +347,35 @@ __device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w,
   }
 }
 
+// float16 bits of a non-negative integer below 2048 (exact): the codebooks' float16 entries, at compile time.
+constexpr uint32_t f16_bits_of(uint32_t n) {
+  if (n == 0) return 0;
+  int e = 0;
+  while ((n >> (e + 1)) != 0) ++e;  // floor(log2 n)
+  return ((uint32_t)(e + 15) << 10) | ((n << (10 - e)) & 0x3FFu);
+}
+template <int N>
+struct HalfGrid {
+  uint64_t v[N];  // entry i's four bytes as float16, the first in the low 16 bits
+};
+template <int N>
+constexpr HalfGrid<N> half_grid(const uint32_t (&g)[N]) {
+  HalfGrid<N> r{};
+  for (int i = 0; i < N; ++i) {
+    const uint64_t lo = f16_bits_of(g[i] & 255) | (f16_bits_of((g[i] >> 8) & 255) << 16);
+    const uint64_t hi = f16_bits_of((g[i] >> 16) & 255) | (f16_bits_of(g[i] >> 24) << 16);
+    r.v[i] = lo | (hi << 32);
+  }
+  return r;
+}
+static constexpr HalfGrid<512> kIq3sHalfGrid = half_grid(kStrataIq3sGrid);
+static constexpr HalfGrid<256> kIq3xxsHalfGrid = half_grid(kStrataIq3xxsGrid);
+
 // The codebook tables in two halves: the constants' loads go out before the rows' (a wait for them is then not
-// a wait for the rows), the LDS entries are written after.
+// a wait for the rows), the LDS entries are written after. The entries are loaded as float16 already.
 template <int KIND>
 struct TableFetch {
-  uint32_t g[2] = {0, 0};
+  uint64_t g[2] = {0, 0};
 };
 template <int KIND, int NT = kThreads>  // NT threads to the workgroup
 __device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
@@ -359,7 +383,7 @@ __device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int i = min(tid + k * NT, FastTraits<KIND>::grid - 1);
-      tf.g[k] = KIND == K_IQ3_S ? kStrataIq3sGrid[i] : kStrataIq3xxsGrid[i];
+      tf.g[k] = KIND == K_IQ3_S ? kIq3sHalfGrid.v[i] : kIq3xxsHalfGrid.v[i];
     }
   }
 }
@@ -369,10 +393,7 @@ __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableF
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int i = tid + k * NT;
-      const uint32_t g = tf.g[k];
-      if (i < FastTraits<KIND>::grid)
-        t.grid[i] = u32x2{pack_h2((float)(g & 255), (float)((g >> 8) & 255)),
-                          pack_h2((float)((g >> 16) & 255), (float)(g >> 24))};
+      if (i < FastTraits<KIND>::grid) t.grid[i] = u32x2{(uint32_t)tf.g[k], (uint32_t)(tf.g[k] >> 32)};
     }
   }
   if (tid < 16) {
@@ -717,9 +738,11 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   TableFetch<KIND> tf;
   fetch_tables<KIND>(tf, tid);
   uint32_t e[4] = {0, 0, 0, 0};
+  const int chunks = (p.pairs + 63) >> 6;  // 64 pair ids a ballot
   if (p.mode == MODE_EXPERT) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
+    for (int c = 0; c < 4; ++c)
+      if (c < chunks) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
   }
   const bool one_x = p.mode == MODE_EXPERT && !GLU && p.share == p.pairs;  // every pair the same token
   // one token for the whole workgroup (one token's routed pairs, a window's first token): read once, coalesced,
@@ -773,6 +796,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
     bool earlier = false;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      if (c >= chunks) break;
       const uint64_t m = __ballot(64 * c + lane < p.pairs && e[c] == expert);
       const int lo_bits = pair - 64 * c;  // bits below are earlier pairs
       const uint64_t below = lo_bits <= 0 ? 0ull : (lo_bits >= 64 ? ~0ull : ((1ull << lo_bits) - 1));
@@ -1026,9 +1050,11 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
   TableFetch<KIND> tf;
   fetch_tables<KIND>(tf, tid);
   uint32_t e[4] = {0, 0, 0, 0};
+  const int chunks = (p.pairs + 63) >> 6;  // 64 pair ids a ballot
   if (routed) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
+    for (int c = 0; c < 4; ++c)
+      if (c < chunks) e[c] = p.idx[min(64 * c + lane, p.pairs - 1)];
   }
   const bool one_x = routed && p.share == p.pairs;  // every pair the same token: one pass writes them all
   u32x4 xv[(kPieces + kThreads - 1) / kThreads];
@@ -1057,6 +1083,7 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
   } else if (!bad) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      if (c >= chunks) break;
       const uint64_t b = __ballot(64 * c + lane < p.pairs && e[c] == expert);
       const int lo_bits = pair - 64 * c;  // bits below are earlier pairs
       const uint64_t below = lo_bits <= 0 ? 0ull : (lo_bits >= 64 ? ~0ull : ((1ull << lo_bits) - 1));
