@@ -371,11 +371,27 @@ constexpr HalfGrid<N> half_grid(const uint32_t (&g)[N]) {
 static constexpr HalfGrid<512> kIq3sHalfGrid = half_grid(kStrataIq3sGrid);
 static constexpr HalfGrid<256> kIq3xxsHalfGrid = half_grid(kStrataIq3xxsGrid);
 
+// float16 bits of a small signed integer (|n| < 2048)
+constexpr uint32_t f16_bits_signed(int n) { return n < 0 ? 0x8000u | f16_bits_of((uint32_t)-n) : f16_bits_of(n); }
+// An IQ4 code byte lo | hi << 4 -> (kvalues[lo], kvalues[hi]) as float16. (Q2_0's table of four (c - 1) is
+// computed in registers instead: loaded, it puts a memory latency ahead of the workgroup barrier, 8 % slower.)
+struct PairCodes {
+  uint32_t v[256];
+};
+constexpr PairCodes pair_codes() {
+  PairCodes t{};
+  for (int i = 0; i < 256; ++i)
+    t.v[i] = f16_bits_signed(kStrataKvaluesIq4nl[i & 15]) | (f16_bits_signed(kStrataKvaluesIq4nl[i >> 4]) << 16);
+  return t;
+}
+static constexpr PairCodes kPairCodes = pair_codes();
+
 // The codebook tables in two halves: the constants' loads go out before the rows' (a wait for them is then not
 // a wait for the rows), the LDS entries are written after. The entries are loaded as float16 already.
 template <int KIND>
 struct TableFetch {
-  uint64_t g[2] = {0, 0};
+  uint64_t g[2] = {0, 0};  // codebook entries
+  uint32_t b = 0;          // IQ4: the pair table's entry
 };
 template <int KIND, int NT = kThreads>  // NT threads to the workgroup
 __device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
@@ -386,6 +402,8 @@ __device__ __forceinline__ void fetch_tables(TableFetch<KIND>& tf, int tid) {
       tf.g[k] = KIND == K_IQ3_S ? kIq3sHalfGrid.v[i] : kIq3xxsHalfGrid.v[i];
     }
   }
+  static_assert(NT >= 256, "one pair-table entry a thread");
+  if constexpr (DirectKind<KIND>::pair_codes > 0) tf.b = kPairCodes.v[min(tid, 255)];
 }
 template <int KIND, int NT = kThreads>
 __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableFetch<KIND>& tf, int tid) {
@@ -401,8 +419,7 @@ __device__ __forceinline__ void store_tables(DirectTables<KIND>& t, const TableF
     t.sign4[tid] = u32x2{m[0], m[1]};
   }
   if constexpr (DirectKind<KIND>::pair_codes > 0) {
-    for (int i = tid; i < 256; i += NT)
-      t.kv2[i] = pack_h2((float)kStrataKvaluesIq4nl[i & 15], (float)kStrataKvaluesIq4nl[i >> 4]);
+    if (tid < 256) t.kv2[tid] = tf.b;
   }
   if constexpr (FastTraits<KIND>::q2 > 0) {
     for (int i = tid; i < 256; i += NT)
