@@ -97,10 +97,23 @@ struct RunPair<K_IQ4_NL> {
   uint16_t d[2];
 };
 
+// Q4_0 and Q5_0: two blocks of 32 weights a lane (Q5_0: their high bits in a word each)
+template <>
+struct RunPair<K_Q4_0> {
+  u32x4 qs[2];
+  uint16_t d[2];
+};
+template <>
+struct RunPair<K_Q5_0> {
+  u32x4 qs[2];
+  uint32_t qh[2];
+  uint16_t d[2];
+};
+
 template <int KIND>
 struct DirectKind {
   static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K ||
-                                 KIND == K_IQ4_XS || KIND == K_IQ4_NL;
+                                 KIND == K_IQ4_XS || KIND == K_IQ4_NL || KIND == K_Q4_0 || KIND == K_Q5_0;
   static constexpr bool any = FastTraits<KIND>::supported || linear;
   // a table of two codebook values a byte (the 16-entry IQ4 codebook)
   static constexpr int pair_codes = KIND == K_IQ4_XS || KIND == K_IQ4_NL ? 256 : 0;
@@ -307,6 +320,23 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
       sc[e] = d * (float)((int)v - 32);
     }
     return RunScale{sc[0], sc[1]};
+  } else if constexpr (KIND == K_Q4_0) {  // w = d * (code - 8), strata_mlx/gguf.py:195-197
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // byte i's low nibble is weight i, its high nibble weight 16 + i
+      bytes_to_h2<8>(f.qs[h][k] & 0x0F0F0F0Fu, w + 2 * k);
+      bytes_to_h2<8>((f.qs[h][k] >> 4) & 0x0F0F0F0Fu, w + 8 + 2 * k);
+    }
+    return RunScale{half_bits(f.d[h]), 0.0f};
+  } else if constexpr (KIND == K_Q5_0) {  // w = d * ((code | high bit << 4) - 16), strata_mlx/gguf.py:198-202
+    const uint32_t qh = f.qh[h];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // weight i's high bit is bit i of qh: four of them spread to bit 4 of bytes
+      const uint32_t hl = ((__builtin_amdgcn_ubfe(qh, 4 * k, 4) * 0x204081u) & 0x01010101u) << 4;
+      const uint32_t hh = ((__builtin_amdgcn_ubfe(qh, 16 + 4 * k, 4) * 0x204081u) & 0x01010101u) << 4;
+      bytes_to_h2<16>((f.qs[h][k] & 0x0F0F0F0Fu) | hl, w + 2 * k);
+      bytes_to_h2<16>(((f.qs[h][k] >> 4) & 0x0F0F0F0Fu) | hh, w + 8 + 2 * k);
+    }
+    return RunScale{half_bits(f.d[h]), 0.0f};
   } else if constexpr (KIND == K_IQ4_NL) {  // w = d * kvalues[code], strata_mlx/blocks.py:69-77
     pair_codes_run(f.qs[h], w, t.kv2);
     return RunScale{half_bits(f.d[h]), 0.0f};
@@ -449,8 +479,11 @@ __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
   } else if constexpr (KIND == K_IQ4_XS) {
     asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.dh), "+v"(f.sl));
     return;
-  } else if constexpr (KIND == K_IQ4_NL) {
+  } else if constexpr (KIND == K_IQ4_NL || KIND == K_Q4_0) {
     asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.d[0]), "+v"(f.d[1]));
+    return;
+  } else if constexpr (KIND == K_Q5_0) {
+    asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.qh[0]), "+v"(f.qh[1]), "+v"(f.d[0]), "+v"(f.d[1]));
     return;
   } else {
 #pragma unroll
@@ -530,9 +563,13 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.a = b;
     o.b = b + 96 + 4 * (jj & 1);
     o.c = b + 104;
-  } else if constexpr (KIND == K_IQ4_NL) {  // two blocks of 18: d @0, qs[16] @2
+  } else if constexpr (KIND == K_IQ4_NL || KIND == K_Q4_0) {  // two blocks of 18: d @0, qs[16] @2
     o.d = j * 36;
     o.qs = j * 36 + 2;
+  } else if constexpr (KIND == K_Q5_0) {  // two blocks of 22: d @0, qh (u32) @2, qs[16] @6
+    o.d = j * 44;
+    o.a = j * 44 + 2;
+    o.qs = j * 44 + 6;
   } else if constexpr (KIND == K_IQ4_XS) {  // d @0, scales_h @2, scales_l[4] @4, qs[128] @8 (run ib @8 + 16 ib)
     const uint32_t b = (j >> 2) * 136, jj = j & 3;
     o.d = b;
@@ -611,11 +648,19 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
     f.hm[0] = load_at<u32x4>(row, lo + o.a);
     f.hm[1] = load_at<u32x4>(row, lo + o.a + 16);
     return;
-  } else if constexpr (KIND == K_IQ4_NL) {
+  } else if constexpr (KIND == K_IQ4_NL || KIND == K_Q4_0) {
     f.d[0] = load_at<uint16_t>(row, lo + o.d);
     f.qs[0] = load_at<u32x4>(row, lo + o.qs);
     f.d[1] = load_at<uint16_t>(row, lo + o.d + 18);
     f.qs[1] = load_at<u32x4>(row, lo + o.qs + 18);
+    return;
+  } else if constexpr (KIND == K_Q5_0) {
+    f.d[0] = load_at<uint16_t>(row, lo + o.d);
+    f.qh[0] = load_at<uint32_t>(row, lo + o.a);
+    f.qs[0] = load_at<u32x4>(row, lo + o.qs);
+    f.d[1] = load_at<uint16_t>(row, lo + o.d + 22);
+    f.qh[1] = load_at<uint32_t>(row, lo + o.a + 22);
+    f.qs[1] = load_at<u32x4>(row, lo + o.qs + 22);
     return;
   } else if constexpr (KIND == K_IQ4_XS) {
     f.dh = load_at<uint32_t>(row, lo + o.d);

@@ -80,7 +80,7 @@ def test_a_matrix_a_pair_gives_the_bits_of_the_stack_at_1536(gpu, kind):
     assert torch.equal(got, want)
 
 
-WINDOW_KINDS = ["IQ3_S", "IQ3_XXS", "Q2_0", "Q3_K", "Q6_K", "Q8_0", "IQ4_XS", "IQ4_NL"]
+WINDOW_KINDS = ["IQ3_S", "IQ3_XXS", "Q2_0", "Q3_K", "Q6_K", "Q8_0", "IQ4_XS", "IQ4_NL", "Q4_0", "Q5_0"]
 
 
 @pytest.mark.parametrize("kind", WINDOW_KINDS)
