@@ -1,6 +1,6 @@
 // The decode matvec for float16 activations, rows read straight into registers (IQ3_S, IQ3_XXS, Q2_0 with
-// their codebooks in LDS; Q3_K, Q4_K, Q6_K, Q8_0 decoded by byte arithmetic; IQ4_XS, IQ4_NL through an LDS table
-// of codebook pairs).
+// their codebooks in LDS; Q3_K, Q4_K, Q6_K, Q8_0, Q4_0, Q5_0 decoded by byte arithmetic; IQ4_XS, IQ4_NL through
+// an LDS table of codebook pairs).
 //
 // A decode call moves tens of megabytes in a few microseconds, so what matters is that every byte is requested
 // at once: a wave's loads go out as soon as it knows its expert, before anything else it does. Nothing is staged
