@@ -1,7 +1,7 @@
 /* strata_gfx950: the expert dequant-matmul path of strata-mlx, for AMD MI355X (gfx950).
  *
  * Activations multiply weights still packed in the GGUF file's own block formats. A block type is
- * given by its GGUF type id (strata_mlx/gguf.py:25-33): Q4_0 2, Q5_0 6, Q8_0 8, Q3_K 11, Q4_K 12,
+ * given by its GGUF type id (strata_mlx/gguf.py:25-33): Q4_0 2, Q5_0 6, Q8_0 8, Q3_K 11, Q4_K 12, Q5_K 13,
  * Q6_K 14, IQ3_XXS 18, IQ4_NL 20, IQ3_S 21, IQ4_XS 23, Q2_0 42. A stack of matrices is laid out as
  * the file lays it out: row r of matrix e starts at byte (e * rows + r) * row_bytes, where
  * row_bytes = cols / weights_per_block * bytes_per_block.

@@ -24,7 +24,8 @@ BLOCK = {"IQ4_NL": (32, 18), "IQ4_XS": (256, 136), "IQ3_S": (256, 110), "IQ3_XXS
          "IQ2_S": (256, 82), "IQ2_XS": (256, 74), "IQ2_XXS": (256, 66), "IQ1_M": (256, 56), "Q2_0": (64, 18),
          "Q3_K": (256, 110)}
 # the dense types of the loader, decoded by the same kernels (strata_mlx/gguf.py:25-33)
-DENSE = {"Q4_0": (32, 18), "Q5_0": (32, 22), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210)}
+DENSE = {"Q4_0": (32, 18), "Q5_0": (32, 22), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q5_K": (256, 176),
+         "Q6_K": (256, 210)}
 # the codebooks of these were not available to this build: the kernels refuse them
 NO_GRID = ("IQ2_S", "IQ2_XS", "IQ2_XXS", "IQ1_M")
 

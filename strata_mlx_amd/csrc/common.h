@@ -26,6 +26,7 @@ static inline int strata_kind_info(int kind, int* per_block, int* block_bytes) {
     case K_IQ4_NL: p = 32; b = 18; break;
     case K_IQ3_S: p = 256; b = 110; break;
     case K_IQ4_XS: p = 256; b = 136; break;
+    case K_Q5_K: p = 256; b = 176; break;
     case K_Q2_0: p = 64; b = 18; break;
     default: return -1;
   }

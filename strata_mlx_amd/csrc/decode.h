@@ -30,6 +30,7 @@ STRATA_TRAITS(K_IQ3_S, 256, 110, 512, 0)
 STRATA_TRAITS(K_IQ3_XXS, 256, 98, 256, 0)
 STRATA_TRAITS(K_Q3_K, 256, 110, 0, 0)
 STRATA_TRAITS(K_Q4_K, 256, 144, 0, 0)
+STRATA_TRAITS(K_Q5_K, 256, 176, 0, 0)
 STRATA_TRAITS(K_Q6_K, 256, 210, 0, 0)
 STRATA_TRAITS(K_Q8_0, 32, 34, 0, 0)
 STRATA_TRAITS(K_Q4_0, 32, 18, 0, 0)
@@ -156,6 +157,20 @@ __device__ __forceinline__ void strata_unpack32(const uint8_t* row, uint32_t n, 
       uint32_t code = (s % 2) ? ((uint32_t)q[i] >> 4) : (q[i] & 15u);
       w[i] = __builtin_fmaf((float)code, scale, bias);  // code * scale is exact: one rounding either way
     }
+  } else if constexpr (KIND == K_Q5_K) {  // gguf.py:207-218: Q4_K's form, a fifth code bit from qh
+    const uint8_t* b = row + (n / 8) * 176;
+    uint32_t s = n % 8;
+    const uint8_t* p = b + 4;
+    uint32_t sc = s < 4 ? (p[s] & 63u) : ((p[s + 4] & 15u) | (((uint32_t)p[s - 4] >> 6) << 4));
+    uint32_t mn = s < 4 ? (p[s + 4] & 63u) : (((uint32_t)p[s + 4] >> 4) | (((uint32_t)p[s] >> 6) << 4));
+    float scale = strata_half_at(b) * (float)sc, bias = -(strata_half_at(b + 2) * (float)mn);
+    const uint8_t* qh = b + 16;
+    const uint8_t* q = b + 48 + 32 * (s / 2);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      uint32_t code = ((s % 2) ? ((uint32_t)q[i] >> 4) : (q[i] & 15u)) | ((((uint32_t)qh[i] >> s) & 1u) << 4);
+      w[i] = __builtin_fmaf((float)code, scale, bias);  // code * scale is exact: one rounding either way
+    }
   } else if constexpr (KIND == K_Q6_K) {  // gguf.py:150-165
     const uint8_t* b = row + (n / 8) * 210;
     uint32_t r8 = n % 8, h = r8 / 4, r = r8 % 4;
@@ -208,6 +223,7 @@ static inline int strata_dispatch_kind(int kind, F&& f) {
     case K_Q2_0: return f(KindTag<K_Q2_0>{});
     case K_IQ4_NL: return f(KindTag<K_IQ4_NL>{});
     case K_IQ4_XS: return f(KindTag<K_IQ4_XS>{});
+    case K_Q5_K: return f(KindTag<K_Q5_K>{});
     case K_IQ3_S: return f(KindTag<K_IQ3_S>{});
     case K_IQ3_XXS: return f(KindTag<K_IQ3_XXS>{});
     case K_Q3_K: return f(KindTag<K_Q3_K>{});

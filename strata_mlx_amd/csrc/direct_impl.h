@@ -97,6 +97,14 @@ struct RunPair<K_IQ4_NL> {
   uint16_t d[2];
 };
 
+template <>
+struct RunPair<K_Q5_K> {
+  u32x4 qs[2];  // as Q4_K's
+  u32x4 qh[2];  // the block's 32 high-bit bytes (sub-block s at bit s)
+  u32x4 sm;
+  uint32_t dd;
+};
+
 // Q4_0 and Q5_0: two blocks of 32 weights a lane (Q5_0: their high bits in a word each)
 template <>
 struct RunPair<K_Q4_0> {
@@ -112,8 +120,9 @@ struct RunPair<K_Q5_0> {
 
 template <int KIND>
 struct DirectKind {
-  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q6_K || KIND == K_Q3_K ||
-                                 KIND == K_IQ4_XS || KIND == K_IQ4_NL || KIND == K_Q4_0 || KIND == K_Q5_0;
+  static constexpr bool linear = KIND == K_Q8_0 || KIND == K_Q4_K || KIND == K_Q5_K || KIND == K_Q6_K ||
+                                 KIND == K_Q3_K || KIND == K_IQ4_XS || KIND == K_IQ4_NL || KIND == K_Q4_0 ||
+                                 KIND == K_Q5_0;
   static constexpr bool any = FastTraits<KIND>::supported || linear;
   // a table of two codebook values a byte (the 16-entry IQ4 codebook)
   static constexpr int pair_codes = KIND == K_IQ4_XS || KIND == K_IQ4_NL ? 256 : 0;
@@ -281,11 +290,17 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
 #pragma unroll
     for (int i = 0; i < 8; ++i) bytes_to_h2<128>(f.q[2 * h + i / 4][i % 4] ^ 0x80808080u, w + 2 * i);
     return RunScale{half_bits(f.d[h]), 0.0f};
-  } else if constexpr (KIND == K_Q4_K) {  // w = code * (d * sc) - dmin * mn, strata_mlx/gguf.py:174-179, 207-217
+  } else if constexpr (KIND == K_Q4_K || KIND == K_Q5_K) {
+    // w = code * (d * sc) - dmin * mn, strata_mlx/gguf.py:174-179, 207-218; Q5_K's codes take bit s of the
+    // high-bit bytes as their fifth bit
+    const int sb = 2 * (j & 3) + h, tb = 8 * (sb & 3);  // sub-block s of the block
 #pragma unroll
-    for (int i = 0; i < 8; ++i) bytes_to_h2<0>((f.qs[i / 4][i % 4] >> (4 * h)) & 0x0F0F0F0Fu, w + 2 * i);
-    // sub-block s = 2 (j % 4) + h of the block: its 6-bit scale and min from the 12 packed bytes p
-    const int sb = 2 * (j & 3) + h, tb = 8 * (sb & 3);
+    for (int i = 0; i < 8; ++i) {
+      uint32_t c = (f.qs[i / 4][i % 4] >> (4 * h)) & 0x0F0F0F0Fu;
+      if constexpr (KIND == K_Q5_K) c |= ((f.qh[i / 4][i % 4] >> sb) & 0x01010101u) << 4;
+      bytes_to_h2<0>(c, w + 2 * i);
+    }
+    // its 6-bit scale and min from the 12 packed bytes p
     const uint32_t b0 = (f.sm[0] >> tb) & 255, b1 = (f.sm[1] >> tb) & 255, b2 = (f.sm[2] >> tb) & 255;
     const bool hi = sb >= 4;
     const uint32_t sc = hi ? ((b2 & 15) | ((b0 >> 6) << 4)) : (b0 & 63);
@@ -365,7 +380,7 @@ __device__ __forceinline__ float dot_n(const uint32_t* w, const uint32_t* x) {
 // The run's sum against 32 activations (16 packed pairs).
 template <int KIND>
 __device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w, const uint32_t* x) {
-  if constexpr (KIND == K_Q4_K) {
+  if constexpr (KIND == K_Q4_K || KIND == K_Q5_K) {
     const uint32_t ones[16] = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
                                0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
                                0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
@@ -469,6 +484,9 @@ __device__ __forceinline__ void opaque(RunPair<KIND>& f) {
   } else if constexpr (KIND == K_Q4_K) {
     asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.sm), "+v"(f.dd));
     return;
+  } else if constexpr (KIND == K_Q5_K) {
+    asm volatile("" : "+v"(f.qs[0]), "+v"(f.qs[1]), "+v"(f.qh[0]), "+v"(f.qh[1]), "+v"(f.sm), "+v"(f.dd));
+    return;
   } else if constexpr (KIND == K_Q6_K) {
     asm volatile("" : "+v"(f.ql[0]), "+v"(f.ql[1]), "+v"(f.qh[0]), "+v"(f.qh[1]), "+v"(f.sc[0]), "+v"(f.sc[1]),
                  "+v"(f.d));
@@ -556,6 +574,12 @@ __device__ __forceinline__ LaneOffsets<KIND> lane_offsets(int j) {
     o.d = b;
     o.qs = b + 16 + 32 * jj;
     o.a = b + 4;
+  } else if constexpr (KIND == K_Q5_K) {  // d, dmin @0, scales[12] @4, qh[32] @16, qs[128] @48
+    const uint32_t b = (j >> 2) * 176, jj = j & 3;
+    o.d = b;
+    o.a = b + 4;
+    o.b = b + 16;
+    o.qs = b + 48 + 32 * jj;
   } else if constexpr (KIND == K_Q3_K) {  // hmask[32] @0, qs[64] @32, scales[12] @96, d @108
     const uint32_t b = (j >> 2) * 110, jj = j & 3;
     o.d = b + 108;
@@ -638,6 +662,14 @@ __device__ __forceinline__ void load_fields(const uint8_t* row, uint32_t lo, con
     f.sm = load_at<u32x4>(row, lo + o.a);
     f.qs[0] = load_at<u32x4>(row, lo + o.qs);
     f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    return;
+  } else if constexpr (KIND == K_Q5_K) {
+    f.dd = load_at<uint32_t>(row, lo + o.d);
+    f.sm = load_at<u32x4>(row, lo + o.a);
+    f.qs[0] = load_at<u32x4>(row, lo + o.qs);
+    f.qs[1] = load_at<u32x4>(row, lo + o.qs + 16);
+    f.qh[0] = load_at<u32x4>(row, lo + o.b);
+    f.qh[1] = load_at<u32x4>(row, lo + o.b + 16);
     return;
   } else if constexpr (KIND == K_Q3_K) {
     f.d = load_at<uint16_t>(row, lo + o.d);
@@ -1214,7 +1246,7 @@ __global__ __launch_bounds__(kThreads, S <= 3 ? 4 : 3) void direct_odd_kernel(Ma
 // direct_odd_kernel.
 template <int KIND>
 int launch_direct_odd(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
-  if constexpr (KIND == K_Q4_K || KIND == K_Q8_0) {
+  if constexpr (KIND == K_Q4_K || KIND == K_Q5_K || KIND == K_Q8_0) {
     return STRATA_ERR_SHAPE;
   } else {
     const int pairs = p.cols / 64;
@@ -1242,7 +1274,7 @@ int launch_direct_odd(MatvecParams& p, int grid_y, int grid_z, hipStream_t strea
 // Q8_0 (its five-step form holds three waves a SIMD and is slower) nor Q4_K (with its run sums of x it spills).
 template <int KIND>
 bool odd_takes(const MatvecParams& p) {
-  if constexpr (KIND == K_Q4_K || KIND == K_Q8_0) return false;
+  if constexpr (KIND == K_Q4_K || KIND == K_Q5_K || KIND == K_Q8_0) return false;
   if (DirectKind<KIND>::linear && p.cols != 40 * 64) return false;
   static const bool on = [] {  // STRATA_ODD_ROWS=0: such rows take direct_decode_kernel (to compare)
     const char* e = getenv("STRATA_ODD_ROWS");

@@ -12,6 +12,7 @@ STRATA_DECLARE(14)
 STRATA_DECLARE(18)
 STRATA_DECLARE(20)
 STRATA_DECLARE(21)
+STRATA_DECLARE(13)
 STRATA_DECLARE(23)
 STRATA_DECLARE(42)
 #undef STRATA_DECLARE
@@ -54,6 +55,7 @@ extern "C" int strata_grouped_matmul(int kind, const void* blocks, int64_t exper
     STRATA_CASE(18)
     STRATA_CASE(20)
     STRATA_CASE(21)
+    STRATA_CASE(13)
     STRATA_CASE(23)
     STRATA_CASE(42)
 #undef STRATA_CASE

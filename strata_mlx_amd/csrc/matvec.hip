@@ -15,6 +15,7 @@ STRATA_DECLARE(14)
 STRATA_DECLARE(18)
 STRATA_DECLARE(20)
 STRATA_DECLARE(21)
+STRATA_DECLARE(13)
 STRATA_DECLARE(23)
 STRATA_DECLARE(42)
 #undef STRATA_DECLARE
@@ -37,6 +38,7 @@ int launch_by_kind(int kind, MatvecParams& p, int x_dtype, int out_dtype, bool g
     STRATA_CASE(18)
     STRATA_CASE(20)
     STRATA_CASE(21)
+    STRATA_CASE(13)
     STRATA_CASE(23)
     STRATA_CASE(42)
 #undef STRATA_CASE
@@ -58,6 +60,7 @@ int dequant_by_kind(int kind, const uint8_t* b, int64_t runs, int per_row, int r
     STRATA_CASE(18)
     STRATA_CASE(20)
     STRATA_CASE(21)
+    STRATA_CASE(13)
     STRATA_CASE(23)
     STRATA_CASE(42)
 #undef STRATA_CASE

@@ -1,4 +1,4 @@
-"""Q3_K, Q4_K, Q6_K, Q8_0, IQ4_XS, IQ4_NL, Q4_0 and Q5_0 decoded in registers (the direct kernel's linear kinds) against the float64 product
+"""Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ4_XS, IQ4_NL, Q4_0 and Q5_0 decoded in registers (the direct kernel's linear kinds) against the float64 product
 of the oracle's weights, at the rows the kernel takes at compile time (64 lanes to a 4096-input row, 32 to 1536
 and 2048) and at run time (16 to 1024): the dense window (test_dense.py:49: 4e-3 relative to the largest output
 for float16), routed pairs with an expert named twice (test_blocks.py:65: 2e-3 relative), gate and up in one
@@ -14,7 +14,7 @@ from strata_mlx_amd import blocks as B
 
 pytestmark = pytest.mark.gpu
 
-LINEAR = ["Q3_K", "Q4_K", "Q6_K", "Q8_0", "IQ4_XS", "IQ4_NL", "Q4_0", "Q5_0"]
+LINEAR = ["Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS", "IQ4_NL", "Q4_0", "Q5_0"]
 
 
 def dev(a, gpu):

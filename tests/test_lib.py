@@ -38,7 +38,7 @@ def test_block_info(kind, per, size):
     assert (p.value, b.value) == (per, size)
 
 
-@pytest.mark.parametrize("kind", ["IQ2_S", "IQ2_XS", "IQ2_XXS", "IQ1_M", "Q5_K"])
+@pytest.mark.parametrize("kind", ["IQ2_S", "IQ2_XS", "IQ2_XXS", "IQ1_M"])
 def test_types_without_kernels_are_refused(kind):
     lib = _lib.library()
     assert lib.strata_block_info(_lib.kind_id(kind), None, None) == _lib.ERR_KIND

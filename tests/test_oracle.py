@@ -168,6 +168,34 @@ def test_q4_k_round_trip():
         np.testing.assert_array_equal(got, want.astype(np.float32))
 
 
+def encode_q5_k(d, dmin, sc, mn, q):
+    """ggml quantize_row_q5_K packing: Q4_K's fields for the low four bits of q (256,) 5-bit codes, their
+    fifth bits in 32 bytes after the scales (weight l of sub-block s at bit s of byte l)."""
+    b4 = encode_q4_k(d, dmin, sc, mn, q & 15)
+    qh = np.zeros(32, np.int64)
+    for s in range(8):
+        qh |= (q[32 * s:32 * s + 32] >> 4) << s
+    return np.concatenate([b4[:16], qh.astype(np.uint8), b4[16:]])
+
+
+def test_q5_k_round_trip():
+    """A misplaced fifth bit (bit l of byte s rather than bit s of byte l) or a dropped one fails here."""
+    rng = np.random.default_rng(2)
+    for _ in range(20):
+        sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        q = rng.integers(0, 32, 256)
+        d, dmin = float(np.float16(rng.uniform(0.001, 0.1))), float(np.float16(rng.uniform(0.001, 0.1)))
+        block = encode_q5_k(d, dmin, sc, mn, q)
+        assert block.size == O.BY_NAME["Q5_K"][2]
+        got = O.dequantize(block, "Q5_K", (1, 256))[0]
+        want = (np.float32(d) * np.repeat(sc, 32).astype(np.float32)) * q.astype(np.float32) \
+            - np.float32(dmin) * np.repeat(mn, 32).astype(np.float32)
+        np.testing.assert_array_equal(got, want.astype(np.float32))
+        # with every fifth bit clear it is the Q4_K block of the same fields
+        low = O.dequantize(encode_q5_k(d, dmin, sc, mn, q & 15), "Q5_K", (1, 256))[0]
+        np.testing.assert_array_equal(low, O.dequantize(encode_q4_k(d, dmin, sc, mn, q & 15), "Q4_K", (1, 256))[0])
+
+
 def encode_q6_k(d, scales, codes):
     """ggml quantize_row_q6_K packing: codes (256,) in -32..31, scales (16,) int8."""
     b = np.zeros(210, np.uint8)
