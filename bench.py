@@ -211,7 +211,8 @@ def cpu_baseline(lins, routes, tokens, budget_s=15.0, max_layers=4):
             flat = r.reshape(-1)
             g = np.stack([w["gate"][int(e)] @ x[p // K].astype(np.float32) for p, e in enumerate(flat)])
             u = np.stack([w["up"][int(e)] @ x[p // K].astype(np.float32) for p, e in enumerate(flat)])
-            h = O.swiglu_rounded(g.astype(np.float16), u.astype(np.float16), np.float16)
+            with np.errstate(over="ignore"):  # a product past float16's range rounds to inf, as on the device
+                h = O.swiglu_rounded(g.astype(np.float16), u.astype(np.float16), np.float16)
             np.stack([w["down"][int(e)] @ h[p].astype(np.float32) for p, e in enumerate(flat)])
             secs += time.perf_counter() - t0
             layers += 1
