@@ -130,6 +130,22 @@ static int unpack32(int kind, const uint8_t* row, uint32_t n, float* w, const ui
         }
         return 0;
     }
+    case 13: { /* Q5_K, gguf.py:207-218: Q4_K's form, the fifth code bit of weight i at bit s of qh[i] */
+        const uint8_t* b = row + (n / 8) * 176;
+        uint32_t s = n % 8;
+        const uint8_t* p = b + 4;
+        uint32_t sc = s < 4 ? (p[s] & 63u) : ((p[s + 4] & 15u) | (((uint32_t)p[s - 4] >> 6) << 4));
+        uint32_t mn = s < 4 ? (p[s + 4] & 63u) : (((uint32_t)p[s + 4] >> 4) | (((uint32_t)p[s] >> 6) << 4));
+        float scale = half_at(b) * (float)sc, bias = -(half_at(b + 2) * (float)mn);
+        const uint8_t* qh = b + 16;
+        const uint8_t* q = b + 48 + 32 * (s / 2);
+        for (uint32_t i = 0; i < 32; ++i) {
+            uint32_t code = ((s % 2) ? ((uint32_t)q[i] >> 4) : (q[i] & 15u)) | ((((uint32_t)qh[i] >> s) & 1u) << 4);
+            volatile float prod = (float)code * scale;
+            w[i] = prod + bias;
+        }
+        return 0;
+    }
     case 14: { /* Q6_K, gguf.py:150-165 */
         const uint8_t* b = row + (n / 8) * 210;
         uint32_t r8 = n % 8, h = r8 / 4, r = r8 % 4;

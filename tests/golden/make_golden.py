@@ -19,6 +19,7 @@ sys.path.insert(0, ROOT)
 from oracle import blocks as O  # noqa: E402
 
 KINDS = ["Q2_0", "IQ4_NL", "IQ4_XS", "IQ3_S", "IQ3_XXS", "Q3_K", "Q4_K", "Q6_K", "Q8_0", "Q4_0", "Q5_0"]
+LATER_KINDS = ["Q5_K"]
 
 
 def main():
@@ -44,6 +45,12 @@ def main():
     out["swiglu/g"], out["swiglu/u"] = g, u
     out["swiglu/h16"] = O.swiglu_rounded(g, u, np.float16)
     out["swiglu/h32"] = O.swiglu_rounded(g.astype(np.float32), u.astype(np.float32), np.float32)
+    # types added later draw from a stream of their own, so the vectors above stay as they were
+    later = np.random.default_rng(20260102)
+    for kind in LATER_KINDS:
+        data = O.random_blocks(kind, 4, later, scale="normal")
+        out[f"{kind}/blocks"] = data
+        out[f"{kind}/weights"] = O.dequantize(data, kind, (1, 4 * O.BY_NAME[kind][1])).astype(np.float32)
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle_vectors.npz")
     np.savez_compressed(path, **out)
     print(path, os.path.getsize(path), "bytes")

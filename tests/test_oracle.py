@@ -61,7 +61,7 @@ def test_ksigns_closed_form():
     assert ((ks & 127) == np.arange(128)).all()
 
 
-KINDS = ["Q2_0", "IQ4_NL", "IQ4_XS", "IQ3_S", "IQ3_XXS", "Q3_K", "Q4_K", "Q6_K", "Q8_0", "Q4_0", "Q5_0"]
+KINDS = ["Q2_0", "IQ4_NL", "IQ4_XS", "IQ3_S", "IQ3_XXS", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q5_0"]
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -369,7 +369,7 @@ def test_the_oracle_still_gives_the_committed_vectors():
     the tile layout and the SwiGLU give the committed numbers, bit for bit."""
     gold = np.load(GOLDEN)
     kinds = sorted({k.split("/")[0] for k in gold.files if k.endswith("/blocks") and "/" in k} - {"matvec"})
-    assert len(kinds) == 11
+    assert len(kinds) == 12
     for kind in kinds:
         data = gold[f"{kind}/blocks"]
         per = O.BY_NAME[kind][1]
