@@ -108,16 +108,51 @@ int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t ex
                        uint32_t* tile_expert, uint32_t* token, uint32_t* where, uint32_t* slot_pair,
                        void* workspace, void* stream);
 
+/* 16-bit rows scaled into float16 by a power of two, for the MFMA kernels below: out[r, c] = a[r, c] / 2^e(r),
+ * e(r) = floor(log2 m(r)) - 14 with m(r) = max_c |a[r, c]| (e = 0 for a row of zeros or one holding an infinity or
+ * NaN), so each row's largest magnitude lands in [2^14, 2^15); row_max[r] = the float bits of m(r). Every value
+ * within 2^31 of m(r) is exact in float16 (all of a bfloat16 row whose values span fewer than 31 binades); smaller
+ * ones round to float16's subnormal steps, an error below 2^-39 m(r). a_dtype BF16, F16 or F32; out float16
+ * (rows, cols). No counterpart in the reference, whose tile kernel takes float16 and float32 only
+ * (strata_mlx/blocks.py:960): this is how bfloat16 activations reach the float16 MFMA exactly. */
+int strata_rows_to_f16(const void* a, int64_t rows, int64_t cols, int a_dtype, void* out, uint32_t* row_max,
+                       void* stream);
+
 /* c[s, :] = W[tile_expert[s / tile]] . a[s, :] for s < n_tiles * tile; a (n_tiles * tile, cols) in
- * a_dtype, c (n_tiles * tile, rows) float32. Tiles naming no expert (>= experts) are skipped and
- * their rows of c are left as they were. F16/BF16 activations go to MFMA as float16 (float32 sums):
- * IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight blocks multiply exact weights (integer codes, the
- * run scale applied to the float32 sums), other types weights rounded to float16. F32 activations
- * multiply exact weights in float32.
+ * a_dtype (F16 or F32), c (n_tiles * tile, rows) float32. Tiles naming no expert (>= experts) are skipped and
+ * their rows of c are left as they were. a_max (F16 only, or NULL): a's rows were scaled by strata_rows_to_f16
+ * and a_max is its row_max; the sums are scaled back exactly. F16 activations go to MFMA as they are (float32
+ * sums): IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight steps multiply exact weights (integer codes times the
+ * run's own scale, exact in float16, with d on the float32 sums; Q2_0 exact while |d| <= 32752), other types
+ * weights rounded to float16. F32 activations multiply exact weights in float32.
  * Replaces tile_matmul + _TILES, strata_mlx/blocks.py:634-654, 583-626. */
 int strata_grouped_matmul(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
-                          const void* a, int a_dtype, const uint32_t* tile_expert, int64_t n_tiles, int64_t tile,
-                          float* c, void* stream);
+                          const void* a, int a_dtype, const uint32_t* a_max, const uint32_t* tile_expert,
+                          int64_t n_tiles, int64_t tile, float* c, void* stream);
+
+/* The gate and up products of a prompt's tiles and the SwiGLU between them, in one launch: for every slot s of a
+ * tile naming an expert e(s) < experts, h[s, r] = silu(g) * u rounded once to h_dtype (F16 or BF16) from float32,
+ * g = G[e(s)][r] . x[token[s]], u = U[e(s)][r] . x[token[s]] (float32 sums; silu(g) * u as mlx-lm's swiglu
+ * computes it on float32 products). x float16 (tokens, cols): as given, or scaled by strata_rows_to_f16 with x_max
+ * its row_max (else NULL). gate / up (experts, rows, cols) stacks; h (n_tiles * tile, rows); token as
+ * strata_route_tiles gives it. Tiles naming no expert leave their rows of h as they were. IQ3_S / IQ3_XXS / Q2_0
+ * stacks with cols a multiple of 256, else STRATA_ERR_KIND (the caller takes strata_grouped_matmul twice).
+ * Replaces the gate and up tile products and the swiglu of _tiled_glu, strata_mlx/blocks.py:684-692. */
+int strata_prompt_gate_up_swiglu(int kind, const void* gate, const void* up, int64_t experts, int64_t rows,
+                                 int64_t cols, const void* x, const uint32_t* x_max, const uint32_t* token,
+                                 const uint32_t* tile_expert, int64_t n_tiles, int64_t tile, void* h, int h_dtype,
+                                 void* stream);
+
+/* The down product of a prompt's tiles written to the pairs: y[slot_pair[s], r] = W[e(s)][r] . h[s] rounded once
+ * to y_dtype (F16 or BF16) from the float32 sum, for every slot s of a tile naming an expert and holding a pair;
+ * y[p, :] = NaN for the pairs p naming no expert (idx[p] >= experts, idx the pairs' experts). h float16
+ * (n_tiles * tile, cols) in slot order, as given or scaled (h_max its row_max, else NULL); y (pairs, rows);
+ * slot_pair as strata_route_tiles gives it. Kinds and shapes as strata_prompt_gate_up_swiglu.
+ * Replaces the down tile product and the [where] gather of _tiled_glu, strata_mlx/blocks.py:693-694. */
+int strata_prompt_down(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols, const void* h,
+                       const uint32_t* h_max, const uint32_t* tile_expert, int64_t n_tiles, int64_t tile,
+                       const uint32_t* slot_pair, const uint32_t* idx, int64_t pairs, void* y, int y_dtype,
+                       void* stream);
 
 /* out[t, r] = W[r, :] . x[t, :] for a float16 W (rows x cols, row-major) and `tokens` rows of x
  * (STRATA_F16 or STRATA_F32); out (tokens, rows) float32. cols must be a multiple of 8. The router's

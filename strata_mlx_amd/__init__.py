@@ -7,7 +7,7 @@ reference's call surface with torch tensors on the GPU:
     blocks   BlockSwitchLinear, BlockSwitchGLU, dequantize, window_matvec, matvec_glu, matvec_separate,
              gate_up_swiglu, tiles_of, tile_matmul, switch_glu          (strata_mlx/blocks.py)
     dense    ScaledLinear, BlockLinear, BlockEmbedding                  (strata_mlx/dense.py)
-    rows     rows_of, GuessRows: listed rows of an output layer         (strata_mlx/rows.py)
+    rows     rows_of: listed rows of an output layer, read in place     (strata_mlx/rows.py)
     fused    WindowLinear (the router), top_k, moe_combine, route       (strata_mlx/fused.py)
     gguf     GGUF, shards, upload, experts, linear, embedding           (strata_mlx/gguf.py, load.py)
     synth    synthetic blocks and Zipf routing for benchmarks and tests

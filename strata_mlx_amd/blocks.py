@@ -437,11 +437,8 @@ def tileable(kind: str, rows: int, cols: int) -> bool:
     return rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % per_block == 0 and kind not in NO_GRID
 
 
-def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
-    """The pairs of `indices` (..., k) laid out in tiles of TOKENS_TILE, each tile one expert's, worked out on the
-    GPU with no host wait: (the expert of each tile, or `experts` for a tile nothing fills; the token of each slot;
-    the slot of each pair), int32, in P // 16 + min(E, P) tiles whatever the routing. An expert's slots go in
-    pair order. strata_mlx/blocks.py:657-681."""
+def _route(indices: torch.Tensor, experts: int) -> tuple:
+    """tiles_of's layout and the pair of each slot (slot_pair, -1 for an empty slot), all int32 on the GPU."""
     k = indices.shape[-1] if indices.ndim else 1
     flat = _idx32(indices)
     pairs = flat.numel()
@@ -450,12 +447,35 @@ def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
     dev = indices.device
     tile_expert = torch.empty(n_tiles, dtype=torch.int32, device=dev)
     token = torch.empty(n_tiles * TOKENS_TILE, dtype=torch.int32, device=dev)
+    slot_pair = torch.empty(n_tiles * TOKENS_TILE, dtype=torch.int32, device=dev)
     where = torch.empty(pairs, dtype=torch.int32, device=dev)
     ws = torch.empty(max(1, lib.strata_route_tiles_workspace(pairs, experts)), dtype=torch.uint8, device=dev)
     _lib.check(lib.strata_route_tiles(flat.data_ptr(), pairs, k, experts, TOKENS_TILE, tile_expert.data_ptr(),
-                                      token.data_ptr(), where.data_ptr(), None, ws.data_ptr(), _lib.stream()),
-               "tiles_of")
-    return tile_expert, token, where
+                                      token.data_ptr(), where.data_ptr(), slot_pair.data_ptr(), ws.data_ptr(),
+                                      _lib.stream()), "tiles_of")
+    return tile_expert, token, where, slot_pair, flat
+
+
+def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
+    """The pairs of `indices` (..., k) laid out in tiles of TOKENS_TILE, each tile one expert's, worked out on the
+    GPU with no host wait: (the expert of each tile, or `experts` for a tile nothing fills; the token of each slot;
+    the slot of each pair), int32, in P // 16 + min(E, P) tiles whatever the routing. An expert's slots go in
+    pair order. strata_mlx/blocks.py:657-681."""
+    return _route(indices, experts)[:3]
+
+
+def rows_to_f16(a: torch.Tensor) -> tuple:
+    """Rows of 16-bit (or float32) activations scaled into float16 by a power of two each, so that each row's
+    largest magnitude lands in [2^14, 2^15): (the float16 rows, each row's largest magnitude as int32 float bits).
+    Exact for every value within 2^31 of its row's largest; the MFMA kernels scale their sums back."""
+    a = a.reshape(-1, a.shape[-1]).contiguous()
+    _lib.require_device(a)
+    rows, cols = a.shape
+    out = torch.empty((rows, cols), dtype=torch.float16, device=a.device)
+    row_max = torch.empty(rows, dtype=torch.int32, device=a.device)
+    _lib.check(_lib.library().strata_rows_to_f16(a.data_ptr(), rows, cols, _lib.dtype_id(a.dtype), out.data_ptr(),
+                                                 row_max.data_ptr(), _lib.stream()), "rows_to_f16")
+    return out, row_max
 
 
 def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, tile_expert: torch.Tensor,
@@ -464,10 +484,11 @@ def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, 
 
     a (P, cols), P a multiple of TOKENS_TILE, every TOKENS_TILE rows for one expert; tile_expert (P / 16,) says
     which, or names no expert (>= experts) for a tile to leave out: its rows of the result are then whatever was
-    in memory (in `out` if given). float16/bfloat16 activations multiply weights rounded to float16 (exact weights
-    for IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight blocks: their codes are exact in float16 and the run
-    scales multiply the float32 sums), float32 ones exact weights; sums are float32. Returns (P, rows) float32.
-    strata_mlx/blocks.py:634-654."""
+    in memory (in `out` if given). float16 activations multiply weights as float16 (exact for IQ3_S / IQ3_XXS /
+    Q2_0 rows of whole 256-weight steps: integer codes times the run's own scale, with d on the float32 sums;
+    rounded to float16 for the other types); bfloat16 rows are first scaled into float16 by a power of two each
+    (rows_to_f16) and the sums scaled back, so they multiply exactly too; float32 activations multiply exact
+    weights in float32. Sums are float32. Returns (P, rows) float32. strata_mlx/blocks.py:634-654."""
     experts, rows, cols = shape
     _flat_u8(blocks)
     a = a.contiguous()
@@ -477,24 +498,59 @@ def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, 
     te = tile_expert.reshape(-1).to(torch.int32).contiguous()
     if te.numel() * TOKENS_TILE != p:
         raise ValueError("one expert to every tile of activations")
+    a_max = None
+    if a.dtype == torch.bfloat16:
+        a, a_max = rows_to_f16(a)
     if out is None:
         out = torch.empty((p, rows), dtype=torch.float32, device=a.device)
     _lib.check(_lib.library().strata_grouped_matmul(
         _lib.kind_id(kind), blocks.data_ptr(), experts, rows, cols, a.data_ptr(), _lib.dtype_id(a.dtype),
-        te.data_ptr(), te.numel(), TOKENS_TILE, out.data_ptr(), _lib.stream()), f"tile_matmul {kind}")
+        _lib.ptr(a_max), te.data_ptr(), te.numel(), TOKENS_TILE, out.data_ptr(), _lib.stream()), f"tile_matmul {kind}")
     return out
 
 
+PROMPT_KINDS = ("IQ3_S", "IQ3_XXS", "Q2_0")  # the kinds of the fused prompt kernels (rows of whole 256-weight steps)
+
+
+def _prompt_fused(lin, dtype: torch.dtype) -> bool:
+    return lin.kind in PROMPT_KINDS and lin.input_dims % 256 == 0 and dtype in (torch.float16, torch.bfloat16)
+
+
 def _tiled_glu(x: torch.Tensor, indices: torch.Tensor, up, gate, down) -> torch.Tensor:
-    """The three products of a prompt's pairs through `tile_matmul`, the pairs in tiles (`tiles_of`); the SwiGLU
-    of the float32 products rounded to the activations' type, as strata_mlx/blocks.py:684-694."""
-    tiles, token, where = tiles_of(indices, gate.num_experts)
-    a = x.reshape(-1, x.shape[-1])[token.long()]
+    """The three products of a prompt's pairs through the tiles (strata_mlx/blocks.py:684-694): the pairs sorted by
+    expert on the GPU, gate and up in one launch with the SwiGLU (float32 products, rounded once to the activations'
+    type) written in slot order, and down written straight to the pairs. bfloat16 rows go to the float16 MFMA
+    scaled by a power of two each (rows_to_f16). Types the fused kernels do not take, and float32, go through
+    tile_matmul and the reference's steps."""
+    tiles, token, where, slot_pair, flat = _route(indices, gate.num_experts)
+    xs = x.reshape(-1, x.shape[-1]).contiguous()
+    lib = _lib.library()
+    n_slots = token.numel()
+    same = (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) == (up.kind, up.output_dims,
+                                                                                 up.input_dims, up.num_experts)
+    if same and _prompt_fused(gate, x.dtype):
+        x16, x_max = rows_to_f16(xs) if x.dtype == torch.bfloat16 else (xs, None)
+        h = torch.empty((n_slots, gate.output_dims), dtype=x.dtype, device=x.device)
+        _lib.check(lib.strata_prompt_gate_up_swiglu(
+            _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), gate.num_experts, gate.output_dims,
+            gate.input_dims, x16.data_ptr(), _lib.ptr(x_max), token.data_ptr(), tiles.data_ptr(), tiles.numel(),
+            TOKENS_TILE, h.data_ptr(), _lib.dtype_id(x.dtype), _lib.stream()), f"prompt gate/up {gate.kind}")
+    else:
+        a = xs[token.long()]
 
-    def product(lin, act):
-        return tile_matmul(lin.blocks, lin.kind, (lin.num_experts, lin.output_dims, lin.input_dims), act, tiles)
+        def product(lin):
+            return tile_matmul(lin.blocks, lin.kind, (lin.num_experts, lin.output_dims, lin.input_dims), a, tiles)
 
-    g, u = product(gate, a), product(up, a)
-    h = (torch.nn.functional.silu(g) * u).to(x.dtype)
-    out = product(down, h)[where.long()].to(x.dtype)
-    return out.reshape(*indices.shape, down.output_dims)
+        h = (torch.nn.functional.silu(product(gate)) * product(up)).to(x.dtype)
+    if _prompt_fused(down, x.dtype):
+        h16, h_max = rows_to_f16(h) if x.dtype == torch.bfloat16 else (h, None)
+        y = torch.empty((flat.numel(), down.output_dims), dtype=x.dtype, device=x.device)
+        _lib.check(lib.strata_prompt_down(
+            _lib.kind_id(down.kind), down.blocks.data_ptr(), down.num_experts, down.output_dims, down.input_dims,
+            h16.data_ptr(), _lib.ptr(h_max), tiles.data_ptr(), tiles.numel(), TOKENS_TILE, slot_pair.data_ptr(),
+            flat.data_ptr(), flat.numel(), y.data_ptr(), _lib.dtype_id(x.dtype), _lib.stream()), f"prompt down {down.kind}")
+    else:
+        c = tile_matmul(down.blocks, down.kind, (down.num_experts, down.output_dims, down.input_dims), h, tiles)
+        y = c[where.long().clamp(min=0)].to(x.dtype)
+        y = torch.where((where >= 0)[:, None], y, torch.full_like(y, float("nan")))  # a pair naming no expert
+    return y.reshape(*indices.shape, down.output_dims)

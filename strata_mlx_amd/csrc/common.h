@@ -85,6 +85,16 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(f16, (uint16_t)h);
 }
 
+// The power of two that puts magnitude m (float bits) into [2^14, 2^15): floor(log2 m) - 14; 0 for m = 0, an
+// infinity or a NaN. A row of activations scaled into float16 was divided by it.
+__device__ __forceinline__ int row_exponent(uint32_t m) {
+  m &= 0x7fffffffu;
+  if (m == 0 || m >= 0x7f800000u) return 0;
+  const int ex = (int)(m >> 23);
+  const int lg = ex ? ex - 127 : (31 - __builtin_clz(m)) - 149;
+  return lg - 14;
+}
+
 #define STRATA_CHECK_LAUNCH()                          \
   do {                                                 \
     hipError_t e_ = hipGetLastError();                 \

@@ -270,15 +270,8 @@ __global__ __launch_bounds__(kThreads, 3) void wave_decode_kernel(MatvecParams p
   }
 }
 
-// Rows a wave's item holds, at most: 8, or STRATA_ROWS_PER_ITEM (1 to 64) to tune the item.
-inline int rows_per_item_limit() {
-  static const int v = [] {
-    const char* e = getenv("STRATA_ROWS_PER_ITEM");
-    const int r = e ? atoi(e) : 8;
-    return (r >= 1 && r <= 64) ? r : 8;
-  }();
-  return v;
-}
+// Rows a wave's item holds, at most.
+constexpr int kRowsPerItem = 8;
 
 inline int device_cus() {
   static int cus[64] = {0};
@@ -314,7 +307,7 @@ int launch_wave_decode(MatvecParams& p, int grid_y, int grid_z, hipStream_t stre
   p.tt = TT;
   p.nz = grid_z;
   const int rows_side = 64 / p.ct;
-  int rt = rows_side * std::max(1, rows_per_item_limit() / rows_side);
+  int rt = rows_side * std::max(1, kRowsPerItem / rows_side);
   while (rt > rows_side && rt * p.row_bytes + 16 > kWLoads * 64 * 16) rt -= rows_side;
   if (rt * p.row_bytes + 16 > kWLoads * 64 * 16) return STRATA_ERR_SHAPE;
   p.rt = rt;

@@ -1062,15 +1062,9 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
   }
 }
 
-// Row steps a unit takes: 4, or STRATA_ROW_STEPS (2 or 4) to tune it.
-inline int row_steps() {
-  static const int v = [] {
-    const char* e = getenv("STRATA_ROW_STEPS");
-    const int r = e ? atoi(e) : 4;
-    return (r == 2 || r == 4) ? r : 4;
-  }();
-  return v;
-}
+// Row steps a unit takes: four, all loaded before the first is decoded (two gave half the fields in flight and
+// were slower; eight hold three waves a SIMD).
+constexpr int kRowSteps = 4;
 
 template <int KIND, bool GLU, bool PAIRED, int TT, int RU, int LT>
 int launch_direct_ru(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
@@ -1102,7 +1096,7 @@ int launch_direct_tt(MatvecParams& p, int grid_y, int grid_z, hipStream_t s) {
   if constexpr (DirectKind<KIND>::linear) {  // their wider fields spill at four row steps
     return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
   } else {
-    if (row_steps() == 2 || (KIND == K_Q2_0 && TT > 1))
+    if (kRowSteps == 2 || (KIND == K_Q2_0 && TT > 1))
       return launch_direct_lt<KIND, GLU, PAIRED, TT, 2>(p, grid_y, grid_z, s);
     return launch_direct_lt<KIND, GLU, PAIRED, TT, 4>(p, grid_y, grid_z, s);
   }
@@ -1276,14 +1270,10 @@ template <int KIND>
 bool odd_takes(const MatvecParams& p) {
   if constexpr (KIND == K_Q4_K || KIND == K_Q5_K || KIND == K_Q8_0) return false;
   if (DirectKind<KIND>::linear && p.cols != 40 * 64) return false;
-  static const bool on = [] {  // STRATA_ODD_ROWS=0: such rows take direct_decode_kernel (to compare)
-    const char* e = getenv("STRATA_ODD_ROWS");
-    return !(e && e[0] == '0');
-  }();
   // listed rows (dense): when the matrix's byte offsets fit 32 bits
   const bool ids_ok = p.row_ids == nullptr ||
                       (p.mode == MODE_DENSE && (int64_t)p.src_rows * p.row_bytes < ((int64_t)1 << 32));
-  return on && p.cols % 64 == 0 && (p.cols / 64 == 24 || p.cols / 64 == 40) && ids_ok &&
+  return p.cols % 64 == 0 && (p.cols / 64 == 24 || p.cols / 64 == 40) && ids_ok &&
          (p.mode == MODE_DENSE || p.pairs <= kDMaxPairs) && p.glu_out == nullptr;
 }
 

@@ -318,15 +318,8 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 6 : 3) void fast_kernel(MatvecP
 }
 
 
-// Rows a thread takes per tile, at most: kRowsPerLane, or STRATA_ROWS_PER_LANE (1, 2, 4 or 8) to tune the tile.
-inline int rows_per_lane_limit() {
-  static const int v = [] {
-    const char* e = getenv("STRATA_ROWS_PER_LANE");
-    const int r = e ? atoi(e) : kRowsPerLane;
-    return (r == 1 || r == 2 || r == 4 || r == 8) ? r : kRowsPerLane;
-  }();
-  return v;
-}
+// Rows a thread takes per tile, at most (fewer where the staged rows or the sums would not fit LDS).
+constexpr int kFastRowsPerLane = kRowsPerLane;
 
 // LDS: tables, queue, at most 32 KB of staged rows (what kLoads loads a thread cover), partial sums; 64 KB in all
 template <int KIND, int TT>
@@ -336,7 +329,7 @@ inline int fast_geometry(MatvecParams& p, size_t* smem) {
   p.ct = p.runs;
   p.rs = kThreads / p.ct;
   const size_t fixed = ((sizeof(FastTables<KIND>) + 15) & ~(size_t)15) + (kMaxQueue + 4) * sizeof(uint32_t);
-  for (int rpl = rows_per_lane_limit(); rpl >= 1; rpl /= 2) {
+  for (int rpl = kFastRowsPerLane; rpl >= 1; rpl /= 2) {
     p.rt = p.rs * rpl;
     p.stage_bytes = ((p.rt * p.row_bytes + 32) + 15) & ~15;
     const size_t red = (size_t)TT * p.rt * (p.ct + 1) * sizeof(float);

@@ -21,19 +21,21 @@ STRATA_DECLARE(42)
 using namespace strata_gemm;
 
 extern "C" int strata_grouped_matmul(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
-                                     const void* a, int a_dtype, const uint32_t* tile_expert, int64_t n_tiles,
-                                     int64_t tile, float* c, void* stream) {
+                                     const void* a, int a_dtype, const uint32_t* a_max, const uint32_t* tile_expert,
+                                     int64_t n_tiles, int64_t tile, float* c, void* stream) {
   int per = 0, bb = 0;
   if (strata_kind_info(kind, &per, &bb)) return STRATA_ERR_KIND;
-  if (rows < 0 || cols <= 0 || cols % per || cols % kKStep || rows > (1 << 30)) return STRATA_ERR_SHAPE;
-  if (a_dtype != DT_F32 && a_dtype != DT_F16 && a_dtype != DT_BF16) return STRATA_ERR_DTYPE;
+  if (rows < 0 || cols <= 0 || cols % per || cols % kKStep || rows > (1 << 24) || cols > (1 << 20))
+    return STRATA_ERR_SHAPE;
+  if (a_dtype != DT_F32 && a_dtype != DT_F16) return STRATA_ERR_DTYPE;
+  if (a_max && a_dtype != DT_F16) return STRATA_ERR_ARG;
   if (tile != 16 || n_tiles < 0 || experts < 0) return STRATA_ERR_ARG;
   if (n_tiles == 0 || rows == 0) return STRATA_OK;
   if (!blocks || !a || !tile_expert || !c) return STRATA_ERR_ARG;
-  if ((n_tiles + kGroupTiles - 1) / kGroupTiles > 65535) return STRATA_ERR_SHAPE;
   GemmParams p = {};
   p.blocks = (const uint8_t*)blocks;
   p.a = a;
+  p.a_max = a_max;
   p.tile_expert = tile_expert;
   p.c = c;
   p.experts = experts;

@@ -75,6 +75,42 @@ __device__ __forceinline__ void stage_bytes(uint8_t* dst, const uint8_t* src, in
   for (; i < chunks; i += nt) d4[i] = __builtin_nontemporal_load(s4 + i);
 }
 
+// The next pairs naming `expert` from `scan` on, at most tt of them, in pair order, into queue; returns how many
+// and moves `scan` past the last one taken. Every thread of the workgroup calls it: a window of blockDim.x pairs
+// at a time, one ballot a wave, the waves' counts added in LDS (wcount: blockDim.x / 64 + 1 ints).
+__device__ __forceinline__ int next_pairs(const uint32_t* idx, int pairs, uint32_t expert, int tt, int& scan,
+                                          uint32_t* queue, int* wcount) {
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, nw = blockDim.x / 64;
+  int n = 0;
+  while (n < tt && scan < pairs) {
+    __syncthreads();  // the last window's counts have been read
+    const int q = scan + tid;
+    const bool hit = q < pairs && idx[q] == expert;
+    const uint64_t m = __ballot(hit);
+    if (lane == 0) wcount[wave] = __popcll(m);
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < nw; ++w) {
+      const int c = wcount[w];
+      before += w < wave ? c : 0;
+      total += c;
+    }
+    const int rank = n + before + __popcll(m & ((1ull << lane) - 1));
+    if (hit && rank < tt) queue[rank] = q;
+    if (hit && rank == tt - 1) wcount[nw] = q + 1;
+    __syncthreads();
+    if (n + total >= tt) {
+      scan = wcount[nw];
+      n = tt;
+    } else {
+      scan += blockDim.x;
+      n += total;
+    }
+  }
+  __syncthreads();  // the queue is written
+  return n;
+}
+
 template <typename XT>
 __device__ __forceinline__ void load_run(const XT* x, float* v) {
 #pragma unroll
@@ -97,8 +133,8 @@ __global__ __launch_bounds__(kThreads, 2) void matvec_kernel(MatvecParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   StrataTables& tab = *reinterpret_cast<StrataTables*>(smem);
   uint32_t* queue = reinterpret_cast<uint32_t*>(smem + sizeof(StrataTables));
-  int* nqueue = reinterpret_cast<int*>(queue + kMaxQueue);
-  uint8_t* stage = smem + sizeof(StrataTables) + (kMaxQueue + 4) * sizeof(uint32_t);
+  int* nqueue = reinterpret_cast<int*>(queue + kMaxQueue);  // also the waves' counts of next_pairs
+  uint8_t* stage = smem + sizeof(StrataTables) + (kMaxQueue + kThreads / 64 + 4) * sizeof(uint32_t);
   float* red = reinterpret_cast<float*>(stage + p.stage_bytes);
 
   const int tid = threadIdx.x, nt = blockDim.x;
@@ -120,21 +156,15 @@ __global__ __launch_bounds__(kThreads, 2) void matvec_kernel(MatvecParams p) {
       return;
     }
     mat = p.blocks[z] + (int64_t)expert * p.mat_bytes;
-    if (tid == 0) {
-      int dup = 0;
-      for (int q = 0; q < first && !dup; ++q) dup = p.idx[q] == expert;
-      *nqueue = dup ? -1 : 0;
-    }
+    int dup = 0;  // an earlier pair names this expert and does its work: every thread looks at a share
+    for (int q = tid; q < first; q += nt) dup |= p.idx[q] == expert;
+    if (__syncthreads_or(dup)) return;
   } else if (p.mode == MODE_PTRS) {
     first = blockIdx.y;
     mat = p.ptrs[first];
-    if (tid == 0) *nqueue = 0;
   } else {
     mat = p.blocks[z];
-    if (tid == 0) *nqueue = 0;
   }
-  __syncthreads();
-  if (*nqueue < 0) return;  // an earlier pair names this expert and does its work
 
   // stage the tile
   if (p.row_ids == nullptr) {
@@ -157,21 +187,23 @@ __global__ __launch_bounds__(kThreads, 2) void matvec_kernel(MatvecParams p) {
   int scan = first;  // expert mode: next pair to look at
   int done_tokens = 0;
   for (;;) {
-    __syncthreads();
-    if (tid == 0) {
-      int n = 0;
-      if (p.mode == MODE_EXPERT) {
-        for (; scan < p.pairs && n < p.tt; ++scan)
-          if (p.idx[scan] == expert) queue[n++] = scan;
-      } else if (p.mode == MODE_PTRS) {
-        if (done_tokens == 0) queue[n++] = first;
-      } else {
-        for (; done_tokens + n < p.tokens && n < p.tt; ++n) queue[n] = done_tokens + n;
+    int nq;
+    if (p.mode == MODE_EXPERT) {
+      nq = next_pairs(p.idx, p.pairs, expert, p.tt, scan, queue, nqueue);
+    } else {
+      __syncthreads();  // the last pass has read the queue
+      if (tid == 0) {
+        int n = 0;
+        if (p.mode == MODE_PTRS) {
+          if (done_tokens == 0) queue[n++] = first;
+        } else {
+          for (; done_tokens + n < p.tokens && n < p.tt; ++n) queue[n] = done_tokens + n;
+        }
+        *nqueue = n;
       }
-      *nqueue = n;
+      __syncthreads();
+      nq = *nqueue;
     }
-    __syncthreads();
-    const int nq = *nqueue;
     if (nq == 0) break;
     done_tokens += nq;
 
@@ -286,7 +318,7 @@ template <int KIND, typename XT, typename OT, bool GLU, int TT>
 int launch_matvec(MatvecParams& p, int grid_y, int grid_z, hipStream_t stream) {
   int rc = geometry(p, TT);
   if (rc) return rc;
-  size_t smem = sizeof(StrataTables) + (kMaxQueue + 4) * sizeof(uint32_t) + p.stage_bytes +
+  size_t smem = sizeof(StrataTables) + (kMaxQueue + kThreads / 64 + 4) * sizeof(uint32_t) + p.stage_bytes +
                 (size_t)TT * p.rt * (p.ct + 1) * sizeof(float);
   dim3 grid((p.rows + p.rt - 1) / p.rt, grid_y, grid_z);
   hipLaunchKernelGGL((matvec_kernel<KIND, XT, OT, GLU, TT>), grid, dim3(kThreads), smem, stream, p);

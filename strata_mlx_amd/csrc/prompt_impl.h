@@ -1,0 +1,303 @@
+// The prompt kernels: grouped dequant-matmuls over tiles of 16 slots, each tile one expert's, on CDNA4 MFMA, for
+// IQ3_S, IQ3_XXS and Q2_0 rows of whole 256-weight steps and float16 activations (strata_mlx/blocks.py:583-694).
+//
+// c[s, :] = W[e(s)] . a[s, :]. A workgroup takes a chunk: the tiles of one expert within an aligned window of NT
+// tiles (the workgroup at the chunk's first tile works, the others exit at once), and a block of rows. Every wave
+// holds two groups of 16 rows: in the SwiGLU form the same 16 rows of gate and of up, otherwise 32 rows of one
+// matrix. The expert's rows are decoded once for all tiles of the chunk.
+//
+// MFMA v_mfma_f32_16x16x32_f16: a (16 slots x 32) x w (32 x 16 rows), float32 sums. Lane (n, g) of a wave gives
+// row n's weights, and it holds the fields of one run pair of the row (64 weights: runs 2g, 2g + 1 of each step of
+// 256 columns; Q6_K's run pairs as the decode kernel takes them), loaded straight from HBM into registers a step
+// ahead. Run h's 32 weights are four MFMAs' worth (8 a lane each); the K order of an MFMA is therefore a
+// permutation of the step's columns, and the slots' activations are read from LDS in that order. The weights reach
+// the MFMA as exact float16 integers with the run's own scale folded in: IQ3_S's (1 + 2s) * grid (at most 465),
+// IQ3_XXS's (2s + 1) * grid (at most 1922), Q2_0's d * (c - 1) (d times -1, 0, 1 or 2, exact unless |d| > 32752).
+// What is common to a row's step (IQ3_S's d, IQ3_XXS's d / 4) multiplies the step's float32 sums, so nothing is
+// rounded before the sums.
+//
+// The activations of a step (16 slots x 256 columns of every tile of the chunk) go to LDS once for the workgroup.
+// Slot s of the chunk reads activation row a_row[s] (the token, for gate and up) or row s (down, whose input is in
+// slot order). Float16 activations only; bfloat16 ones are given as rows scaled into float16 by a power of two
+// (strata_rows_to_f16: a row's largest magnitude into [2^14, 2^15)), with a_max holding each row's largest
+// magnitude, and the sums are scaled back by that power exactly.
+//
+// Work goes to workgroups so that every row block of a tile runs on one XCD (workgroup i runs on XCD i % 8): the
+// tile's activations are then read into one L2.
+#pragma once
+#include "direct_impl.h"
+
+namespace strata_prompt {
+
+using strata_mv::DirectTables;
+using strata_mv::LaneOffsets;
+using strata_mv::RunPair;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kStep = 256;           // columns a K step: a 256-weight block of every row (four Q2_0 blocks)
+constexpr int kPitch = kStep + 8;    // float16 a slot's step in LDS: 16 slots' 16-byte reads fall on distinct banks
+constexpr int kXcds = 8;             // workgroup i runs on XCD i % 8
+constexpr int kMinWaves = 3;         // waves a SIMD the kernels are built for (at most 168 VGPRs)
+
+enum PromptMode : int { PM_C32 = 0, PM_GLU = 1, PM_SCATTER = 2 };
+
+struct PromptParams {
+  const uint8_t* blocks[2];     // the stacks: gate and up (SwiGLU form), else blocks[0]
+  const f16* a;                 // float16 activations (a_rows x cols)
+  const uint32_t* a_row;        // the activation row of each slot, or null (slot s reads row s)
+  const uint32_t* a_max;        // scaled rows: each row's largest magnitude (float bits), or null
+  const uint32_t* tile_expert;  // expert of each tile (>= experts: a tile to leave out)
+  const uint32_t* slot_pair;    // scatter form: the output row of each slot (0xffffffff: none)
+  void* out;                    // C32: float (slots x rows); SwiGLU: h (slots x rows); scatter: y (pairs x rows)
+  int64_t experts, mat_bytes;
+  int rows, cols, row_bytes, n_tiles, row_blocks;
+};
+
+// The run's own scale folded into its 16 packed float16 pairs of integers (exact, see above).
+template <int KIND>
+__device__ __forceinline__ void fold_run(const RunPair<KIND>& f, int h, int g, uint32_t (&w)[16]) {
+  f16 m;
+  if constexpr (KIND == K_IQ3_S) {
+    m = (f16)(float)(1 + 2 * __builtin_amdgcn_ubfe((uint32_t)f.sc, 8 * (g & 1) + 4 * h, 4));
+  } else if constexpr (KIND == K_IQ3_XXS) {
+    m = (f16)(float)(1 + 2 * (f.aux[h] >> 28));
+  } else {
+    m = __builtin_bit_cast(f16, (uint16_t)f.d);
+  }
+  const h2v m2 = h2v{m, m};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, w[i]) * m2);
+}
+
+// What multiplies a row's whole step: IQ3_S d, IQ3_XXS d / 4 (strata_mlx/blocks.py:89-116); Q2_0 has none left.
+template <int KIND>
+__device__ __forceinline__ float step_scale(const RunPair<KIND>& f) {
+  if constexpr (KIND == K_IQ3_S) return strata_mv::half_bits(f.d);
+  if constexpr (KIND == K_IQ3_XXS) return strata_mv::half_bits(f.d) * 0.25f;
+  return 1.0f;
+}
+template <int KIND>
+constexpr bool has_step_scale() {
+  return KIND == K_IQ3_S || KIND == K_IQ3_XXS;
+}
+
+// Column (within the step) of the first of the 8 weights lane group g gives MFMA (h, q): run run_of(g, h), its
+// weights 8q .. 8q + 7.
+template <int KIND>
+__device__ __forceinline__ int a_col(int g, int h, int q) {
+  return 32 * strata_mv::run_of<KIND>(g, h) + 8 * q;
+}
+
+template <typename OT>
+__device__ __forceinline__ void store_out(OT* p, float v) {
+  *p = from_f32<OT>(v);
+}
+
+// silu(g) * u in float32, as mlx-lm's swiglu computes it on the float32 products (strata_mlx/blocks.py:692).
+__device__ __forceinline__ float swiglu_f32(float g, float u) {
+  const float s = 1.0f / (1.0f + expf(-g));
+  return (g * s) * u;
+}
+
+template <int KIND, int MODE, typename OT, int WAVES, int NT>
+__global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptParams p) {
+  constexpr int kThreadsWg = 64 * WAVES;
+  constexpr bool kGlu = MODE == PM_GLU;
+  constexpr int kRowsWave = kGlu ? 16 : 32;
+  constexpr int kChunks = NT * 16 * (kStep / 8);  // 16-byte pieces of the chunk's activations a step
+  constexpr int kLoads = kChunks / kThreadsWg;     // a thread's
+  static_assert(kChunks % kThreadsWg == 0, "whole pieces a thread");
+  __shared__ DirectTables<KIND> tab;
+  __shared__ __attribute__((aligned(16))) f16 a_lds[NT * 16 * kPitch];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // (tile, row block) of this workgroup: every row block of a tile on the XCD of the tile's index
+  const int L = blockIdx.x, xcd = L % kXcds, s = L / kXcds;
+  const int t0 = kXcds * (s / p.row_blocks) + xcd, rb = s % p.row_blocks;
+  if (t0 >= p.n_tiles) return;
+  const uint32_t e = p.tile_expert[t0];
+  if (e >= (uint64_t)p.experts) return;  // a tile nothing fills: left out
+  if (t0 % NT != 0 && p.tile_expert[t0 - 1] == e) return;  // a tile of a chunk that starts before it
+  const int wend = min((t0 / NT + 1) * NT, p.n_tiles);
+  int nt = 1;
+#pragma unroll
+  for (int i = 1; i < NT; ++i)
+    if (t0 + i < wend && nt == i && p.tile_expert[t0 + i] == e) nt = i + 1;
+  nt = __builtin_amdgcn_readfirstlane(nt);
+
+  {  // the codebooks, read after the K loop's first barrier
+    strata_mv::TableFetch<KIND> tf;
+    strata_mv::fetch_tables<KIND, kThreadsWg>(tf, tid);
+    strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
+  }
+
+  // the lane's rows and fields
+  const int n = lane & 15, g = lane >> 4;
+  const int r0 = rb * kRowsWave * WAVES + wave * kRowsWave;
+  const int row0 = r0 + n, row1 = kGlu ? r0 + n : r0 + 16 + n;
+  const uint8_t* mat0 = p.blocks[0] + (int64_t)e * p.mat_bytes;
+  const uint8_t* mat1 = kGlu ? p.blocks[1] + (int64_t)e * p.mat_bytes : mat0;
+  const uint32_t off0 = (uint32_t)min(row0, p.rows - 1) * (uint32_t)p.row_bytes;
+  const uint32_t off1 = (uint32_t)min(row1, p.rows - 1) * (uint32_t)p.row_bytes;
+  const LaneOffsets<KIND> o = strata_mv::lane_offsets<KIND>(g);
+  const int nsteps = p.cols / kStep;
+  const uint32_t step_bytes = (uint32_t)(p.row_bytes / nsteps);
+
+  // the thread's pieces of the activations: (tile, slot, piece) -> global row and LDS place
+  const f16* arow[kLoads];
+  int adst[kLoads];
+  bool aon[kLoads];
+#pragma unroll
+  for (int q = 0; q < kLoads; ++q) {
+    const int c = tid + q * kThreadsWg;
+    const int i = c / (16 * (kStep / 8)), m = (c / (kStep / 8)) % 16, piece = c % (kStep / 8);
+    const int slot = (t0 + i) * 16 + m;
+    aon[q] = i < nt;
+    const uint32_t r = aon[q] ? (p.a_row ? p.a_row[slot] : (uint32_t)slot) : 0u;
+    arow[q] = p.a + (int64_t)r * p.cols + 8 * piece;
+    adst[q] = (i * 16 + m) * kPitch + 8 * piece;
+  }
+  u32x4 av[kLoads];
+#pragma unroll
+  for (int q = 0; q < kLoads; ++q)
+    if (aon[q]) av[q] = *reinterpret_cast<const u32x4*>(arow[q]);
+
+  RunPair<KIND> f[2][2];  // [step parity][row group]
+  strata_mv::load_fields<KIND>(mat0, off0, o, f[0][0]);
+  strata_mv::load_fields<KIND>(mat1, off1, o, f[0][1]);
+
+  f32x4 acc[2][NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) acc[0][i] = acc[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < nsteps; kb += 2) {
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+      const int k = kb + sp;
+      if (k < nsteps) {
+        // the next step's fields (past the last step, the last again: unconditional loads)
+        const uint32_t nx = (uint32_t)min(k + 1, nsteps - 1) * step_bytes;
+        strata_mv::load_fields<KIND>(mat0, off0 + nx, o, f[sp ^ 1][0]);
+        strata_mv::load_fields<KIND>(mat1, off1 + nx, o, f[sp ^ 1][1]);
+        __syncthreads();  // every wave has read the last step's activations (and the tables are written)
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q)
+          if (aon[q]) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+        if (k + 1 < nsteps) {
+#pragma unroll
+          for (int q = 0; q < kLoads; ++q)
+            if (aon[q]) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 1) * kStep);
+        }
+        __syncthreads();
+
+        f32x4 part[2][NT];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) part[0][i] = part[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t w0[16], w1[16];
+          strata_mv::decode_run<KIND>(f[sp][0], h, g, w0, tab);
+          fold_run<KIND>(f[sp][0], h, g, w0);
+          strata_mv::decode_run<KIND>(f[sp][1], h, g, w1, tab);
+          fold_run<KIND>(f[sp][1], h, g, w1);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[4 * q], w0[4 * q + 1], w0[4 * q + 2], w0[4 * q + 3]});
+            const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[4 * q], w1[4 * q + 1], w1[4 * q + 2], w1[4 * q + 3]});
+            const int col = a_col<KIND>(g, h, q);
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+              if (i < nt) {
+                const f16x8 a8 = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + col);
+                f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
+                f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
+                p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b0, p0, 0, 0, 0);
+                p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b1, p1, 0, 0, 0);
+              }
+            }
+          }
+        }
+        if constexpr (has_step_scale<KIND>()) {
+          const float s0 = step_scale<KIND>(f[sp][0]), s1 = step_scale<KIND>(f[sp][1]);
+#pragma unroll
+          for (int i = 0; i < NT; ++i) {
+            if (i < nt) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                acc[0][i][j] = __builtin_fmaf(s0, part[0][i][j], acc[0][i][j]);
+                acc[1][i][j] = __builtin_fmaf(s1, part[1][i][j], acc[1][i][j]);
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // lane (n, g) holds slots 4g + j of each tile, for rows row0 and row1
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    if (i < nt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int slot = (t0 + i) * 16 + 4 * g + j;
+        float v0 = acc[0][i][j], v1 = acc[1][i][j];
+        if (p.a_max != nullptr) {
+          const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
+          const int ex = row_exponent(p.a_max[r]);
+          v0 = __builtin_ldexpf(v0, ex);
+          v1 = __builtin_ldexpf(v1, ex);
+        }
+        if constexpr (MODE == PM_C32) {
+          float* c = reinterpret_cast<float*>(p.out) + (int64_t)slot * p.rows;
+          if (row0 < p.rows) c[row0] = v0;
+          if (row1 < p.rows) c[row1] = v1;
+        } else if constexpr (MODE == PM_GLU) {
+          if (row0 < p.rows) store_out<OT>(reinterpret_cast<OT*>(p.out) + (int64_t)slot * p.rows + row0,
+                                           swiglu_f32(v0, v1));
+        } else {
+          const uint32_t pr = p.slot_pair[slot];
+          if (pr != 0xffffffffu) {
+            OT* y = reinterpret_cast<OT*>(p.out) + (int64_t)pr * p.rows;
+            if (row0 < p.rows) store_out<OT>(y + row0, v0);
+            if (row1 < p.rows) store_out<OT>(y + row1, v1);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int MODE>
+constexpr int rows_per_wg(int waves) {
+  return (MODE == PM_GLU ? 16 : 32) * waves;
+}
+
+// Whether the prompt kernels take a stack: a type they decode, rows of whole 256-weight steps.
+inline bool prompt_takes(int kind, int64_t cols) {
+  return (kind == K_IQ3_S || kind == K_IQ3_XXS || kind == K_Q2_0) && cols % kStep == 0 && cols > 0;
+}
+
+constexpr int kWaves = 4;
+constexpr int kTiles = 2;
+
+template <int KIND, int MODE, typename OT>
+int launch_prompt(PromptParams& p, hipStream_t s) {
+  constexpr int rpw = rows_per_wg<MODE>(kWaves);
+  p.row_blocks = (p.rows + rpw - 1) / rpw;
+  const int64_t tiles = (p.n_tiles + kXcds - 1) / kXcds * kXcds;
+  const int64_t grid = tiles * p.row_blocks;
+  if (grid <= 0) return STRATA_OK;
+  if (grid > 0x7fffffff) return STRATA_ERR_SHAPE;
+  hipLaunchKernelGGL((prompt_kernel<KIND, MODE, OT, kWaves, kTiles>), dim3((unsigned)grid), dim3(64 * kWaves), 0, s,
+                     p);
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
+}  // namespace strata_prompt

@@ -8,8 +8,11 @@
                    (blocks.q3k_planes), as the reference holds them.
     BlockEmbedding rows of an embedding decoded when their tokens come (dense.py:245-258).
 
-Up to MAX_TOKENS tokens a product is a window of the matvec kernel (each block decoded once for every token); a
-longer chunk multiplies the dequantized weights as floats (torch's GEMM), as the reference does.
+Up to MAX_TOKENS tokens a product is a window of the matvec kernel (each block decoded once for every token). A
+longer chunk (a prompt's) goes through the tile kernels as a stack of one matrix: its tokens in tiles of 16, every
+weight tile decoded into LDS once for 16 tiles and multiplied on MFMA with float32 sums (the reference multiplies
+float weights kept for the purpose, dense.py:141-157; here no float copy of the layer is made). bfloat16 tokens
+are scaled into float16 rows by a power of two each, exactly, and the sums scaled back.
 """
 
 import torch
@@ -90,9 +93,25 @@ class BlockLinear:
                 out = out[:, row_ids.reshape(-1).long()]
         elif tokens <= MAX_TOKENS or row_ids is not None:
             out = B.window_matvec(self.blocks, self.kind, rows, cols, x2, row_ids=row_ids)
+        elif B.tileable(self.kind, rows, cols):
+            out = tiled_chunk(self.blocks, self.kind, rows, cols, x2)
         else:
             out = x2 @ self.floats(x.dtype).T
         return out.reshape(*lead, out.shape[-1])
+
+
+def tiled_chunk(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor) -> torch.Tensor:
+    """out[t] = W . x[t] for a chunk of tokens x (tokens, cols) through the tile kernels, W one matrix of blocks:
+    (tokens, rows) in x's type, float32 sums."""
+    tokens = x.shape[0]
+    tiles = (tokens + B.TOKENS_TILE - 1) // B.TOKENS_TILE
+    a = x
+    if tiles * B.TOKENS_TILE != tokens:  # the last tile's empty slots multiply zeros
+        a = torch.zeros((tiles * B.TOKENS_TILE, cols), dtype=x.dtype, device=x.device)
+        a[:tokens] = x
+    te = torch.zeros(tiles, dtype=torch.int32, device=x.device)
+    c = B.tile_matmul(blocks, kind, (1, rows, cols), a, te)
+    return c[:tokens].to(x.dtype)
 
 
 class ScaledLinear(BlockLinear):

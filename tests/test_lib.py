@@ -25,7 +25,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.strata_abi_version() == 1
+    assert lib.strata_abi_version() == 2
 
 
 @pytest.mark.parametrize("kind, per, size", [("Q2_0", 64, 18), ("IQ3_S", 256, 110), ("IQ3_XXS", 256, 98),
@@ -57,6 +57,20 @@ def test_arguments_are_checked_before_any_launch():
     assert lib.strata_expert_matvec(q, 1, 4, 8, 16384, 1, 4, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # > 8192 cols
     assert lib.strata_expert_matvec(99, 1, 4, 8, 256, 1, 4, 1, 1, 1, 1, None) == _lib.ERR_KIND
     assert lib.strata_dense_matvec(q, 1, 8, 256, 1, 1, 1, 1, 2, None, 0, None) == _lib.ERR_DTYPE  # f16 -> bf16
+    x3 = _lib.kind_id("IQ3_XXS")
+    assert lib.strata_grouped_matmul(x3, 1, 4, 64, 256, 1, 2, None, 1, 1, 16, 1, None) == _lib.ERR_DTYPE  # bf16 a
+    assert lib.strata_grouped_matmul(x3, 1, 4, 64, 256, 1, 0, 1, 1, 1, 16, 1, None) == _lib.ERR_ARG  # a_max on f32
+    assert lib.strata_rows_to_f16(1, 4, 64, 7, 1, 1, None) == _lib.ERR_DTYPE
+    assert lib.strata_rows_to_f16(0, 0, 64, 2, 0, 0, None) == _lib.OK  # no rows
+    gu = lib.strata_prompt_gate_up_swiglu
+    assert gu(_lib.kind_id("Q4_K"), 1, 1, 4, 64, 256, 1, None, 1, 1, 1, 16, 1, 1, None) == _lib.ERR_KIND
+    assert gu(x3, 1, 1, 4, 64, 320, 1, None, 1, 1, 1, 16, 1, 1, None) == _lib.ERR_SHAPE  # not whole blocks
+    assert gu(x3, 1, 1, 4, 64, 256, 1, None, 1, 1, 1, 16, 1, 0, None) == _lib.ERR_DTYPE  # float32 h
+    assert gu(x3, 1, 1, 4, 64, 256, 1, None, 1, 1, 1, 8, 1, 1, None) == _lib.ERR_ARG  # tiles of 8
+    assert gu(x3, 0, 1, 4, 64, 256, 1, None, 1, 1, 1, 16, 1, 1, None) == _lib.ERR_ARG  # null gate
+    dn = lib.strata_prompt_down
+    assert dn(x3, 1, 4, 64, 256, 1, None, 1, 1, 16, 1, 1, -1, 1, 1, None) == _lib.ERR_ARG  # negative pairs
+    assert dn(x3, 1, 4, 64, 256, 1, None, 1, 1, 16, 1, 0, 4, 1, 1, None) == _lib.ERR_ARG  # null idx
     with pytest.raises(ValueError):
         _lib.check(_lib.ERR_SHAPE, "x")
     with pytest.raises(RuntimeError):
