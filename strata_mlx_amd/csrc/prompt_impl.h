@@ -1,20 +1,21 @@
 // The prompt kernels: grouped dequant-matmuls over tiles of 16 slots, each tile one expert's, on CDNA4 MFMA, for
 // IQ3_S, IQ3_XXS and Q2_0 rows of whole 256-weight steps and float16 activations (strata_mlx/blocks.py:583-694).
 //
-// c[s, :] = W[e(s)] . a[s, :]. A workgroup takes a chunk: the tiles of one expert within an aligned window of NT
-// tiles (the workgroup at the chunk's first tile works, the others exit at once), and a block of rows. Every wave
-// holds two groups of 16 rows: in the SwiGLU form the same 16 rows of gate and of up, otherwise 32 rows of one
-// matrix. The expert's rows are decoded once for all tiles of the chunk.
+// c[s, :] = W[e(s)] . a[s, :]. A workgroup (4 waves) takes a chunk, the tiles of one expert within an aligned
+// window of NT = 2 tiles (the workgroup at the chunk's first tile works, the others exit at once), and a block of
+// rows. Every wave holds two groups of 16 rows: in the SwiGLU form the same 16 rows of gate and of up, otherwise 32
+// rows of one matrix. The expert's rows are decoded once for all tiles of the chunk, and the body is compiled for
+// each chunk size, so no branch sits between the MFMAs.
 //
 // MFMA v_mfma_f32_16x16x32_f16: a (16 slots x 32) x w (32 x 16 rows), float32 sums. Lane (n, g) of a wave gives
 // row n's weights, and it holds the fields of one run pair of the row (64 weights: runs 2g, 2g + 1 of each step of
-// 256 columns; Q6_K's run pairs as the decode kernel takes them), loaded straight from HBM into registers a step
-// ahead. Run h's 32 weights are four MFMAs' worth (8 a lane each); the K order of an MFMA is therefore a
-// permutation of the step's columns, and the slots' activations are read from LDS in that order. The weights reach
-// the MFMA as exact float16 integers with the run's own scale folded in: IQ3_S's (1 + 2s) * grid (at most 465),
-// IQ3_XXS's (2s + 1) * grid (at most 1922), Q2_0's d * (c - 1) (d times -1, 0, 1 or 2, exact unless |d| > 32752).
-// What is common to a row's step (IQ3_S's d, IQ3_XXS's d / 4) multiplies the step's float32 sums, so nothing is
-// rounded before the sums.
+// 256 columns), loaded straight from HBM into registers a step ahead. Run h's 32 weights are four MFMAs' worth (8 a
+// lane each); the K order of an MFMA is therefore a permutation of the step's columns, and the slots' activations
+// are read from LDS in that order. The weights reach the MFMA as exact float16 integers with the run's own scale
+// folded in: IQ3_S's (1 + 2s) * grid (at most 465), IQ3_XXS's (2s + 1) * grid (at most 1922), Q2_0's d * (c - 1)
+// (d times -1, 0, 1 or 2, exact unless |d| > 32752). What is common to a row's step (IQ3_S's d, IQ3_XXS's d / 4)
+// multiplies the step's float32 sums, so nothing is rounded before the sums. Codebook entries come from LDS as
+// float16 magnitudes; their signs are set in registers (no sign table in LDS).
 //
 // The activations of a step (16 slots x 256 columns of every tile of the chunk) go to LDS once for the workgroup.
 // Slot s of the chunk reads activation row a_row[s] (the token, for gate and up) or row s (down, whose input is in
@@ -22,8 +23,9 @@
 // (strata_rows_to_f16: a row's largest magnitude into [2^14, 2^15)), with a_max holding each row's largest
 // magnitude, and the sums are scaled back by that power exactly.
 //
-// Work goes to workgroups so that every row block of a tile runs on one XCD (workgroup i runs on XCD i % 8): the
-// tile's activations are then read into one L2.
+// Workgroup i runs on XCD i % 8. Windows of NT tiles go to the XCDs in turn, and every row block of a window's
+// tiles runs on the window's XCD: the chunks (one or two a window) spread evenly over the XCDs, and a tile's
+// activations are read into one L2.
 #pragma once
 #include "direct_impl.h"
 
@@ -84,6 +86,59 @@ constexpr bool has_step_scale() {
   return KIND == K_IQ3_S || KIND == K_IQ3_XXS;
 }
 
+// The signs of 8 weights (bits of s8, weight j at bit j) put on 8 float16 magnitudes (two codebook entries, whose sign
+// bits are clear), in registers: s8 goes to both 16-bit halves of a word, a packed shift a word brings weight
+// (2i, 2i + 1)'s bits to bit 15 of each half, and an and-or sets them.
+__device__ __forceinline__ void put_signs(uint32_t s8, const u32x2& g0, const u32x2& g1, uint32_t* w) {
+  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+  const us2 d = __builtin_bit_cast(us2, s8 * 0x10001u);
+  const uint32_t m0 = __builtin_bit_cast(uint32_t, (us2)(d << us2{15, 14}));
+  const uint32_t m1 = __builtin_bit_cast(uint32_t, (us2)(d << us2{13, 12}));
+  const uint32_t m2 = __builtin_bit_cast(uint32_t, (us2)(d << us2{11, 10}));
+  const uint32_t m3 = __builtin_bit_cast(uint32_t, (us2)(d << us2{9, 8}));
+  w[0] = (m0 & 0x80008000u) | g0[0];
+  w[1] = (m1 & 0x80008000u) | g0[1];
+  w[2] = (m2 & 0x80008000u) | g1[0];
+  w[3] = (m3 & 0x80008000u) | g1[1];
+}
+
+// Run h of the lane's run pair g: 16 packed float16 pairs, the run's scale and signs folded in (exact).
+template <int KIND>
+__device__ __forceinline__ void decode_folded(const RunPair<KIND>& f, int h, int g, uint32_t (&w)[16],
+                                              const DirectTables<KIND>& t) {
+  if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116
+    const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
+    const uint32_t aux = f.aux[h];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {  // group pair l: groups 2l, 2l + 1, signs ksigns[7 bits of aux]
+      const uint32_t q = l < 2 ? qs0 : qs1;
+      const u32x2 g0 = t.grid[(q >> (16 * (l & 1))) & 255];
+      const u32x2 g1 = t.grid[(q >> (16 * (l & 1) + 8)) & 255];
+      const uint32_t s7 = __builtin_amdgcn_ubfe(aux, 7 * l, 7);
+      const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);  // the parity in bit 7
+      put_signs(s8, g0, g1, w + 4 * l);
+    }
+  } else if constexpr (KIND == K_IQ3_S) {  // strata_mlx/blocks.py:89-102
+    const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
+    const uint32_t qh = (f.qh >> (8 * h)) & 255, sg = f.sg[h];
+    const uint32_t hb0 = (__builtin_amdgcn_ubfe(qh, 0, 4) * 0x204081u) & 0x01010101u;
+    const uint32_t hb1 = (__builtin_amdgcn_ubfe(qh, 4, 4) * 0x204081u) & 0x01010101u;
+    const uint32_t i01 = __builtin_amdgcn_perm(hb0, qs0, 0x05010400u), i23 = __builtin_amdgcn_perm(hb0, qs0, 0x07030602u);
+    const uint32_t i45 = __builtin_amdgcn_perm(hb1, qs1, 0x05010400u), i67 = __builtin_amdgcn_perm(hb1, qs1, 0x07030602u);
+    const uint32_t three = 3;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {  // group pair l: groups 2l, 2l + 1 (index words i01 .. i67), signs byte l
+      const uint32_t iw = l == 0 ? i01 : l == 1 ? i23 : l == 2 ? i45 : i67;
+      const u32x2 g0 = strata_mv::lds_entry(t.grid, strata_mv::word_shl<0>(iw, three));
+      const u32x2 g1 = strata_mv::lds_entry(t.grid, strata_mv::word_shl<1>(iw, three));
+      put_signs((sg >> (8 * l)) & 255u, g0, g1, w + 4 * l);
+    }
+  } else {
+    strata_mv::decode_run<KIND>(f, h, g, w, t);
+  }
+  fold_run<KIND>(f, h, g, w);
+}
+
 // Column (within the step) of the first of the 8 weights lane group g gives MFMA (h, q): run run_of(g, h), its
 // weights 8q .. 8q + 7.
 template <int KIND>
@@ -102,39 +157,18 @@ __device__ __forceinline__ float swiglu_f32(float g, float u) {
   return (g * s) * u;
 }
 
-template <int KIND, int MODE, typename OT, int WAVES, int NT>
-__global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptParams p) {
+// One chunk of exactly NTC tiles (NTC at compile time: no per-tile branches between the MFMAs).
+template <int KIND, int MODE, typename OT, int WAVES, int NTC>
+__device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTables<KIND>& tab,
+                                          f16* a_lds, uint32_t e, int t0, int rb, int tid,
+                                          int wave) {
   constexpr int kThreadsWg = 64 * WAVES;
   constexpr bool kGlu = MODE == PM_GLU;
   constexpr int kRowsWave = kGlu ? 16 : 32;
-  constexpr int kChunks = NT * 16 * (kStep / 8);  // 16-byte pieces of the chunk's activations a step
-  constexpr int kLoads = kChunks / kThreadsWg;     // a thread's
+  constexpr int kChunks = NTC * 16 * (kStep / 8);  // 16-byte pieces of the chunk's activations a step
+  constexpr int kLoads = kChunks / kThreadsWg;      // a thread's
   static_assert(kChunks % kThreadsWg == 0, "whole pieces a thread");
-  __shared__ DirectTables<KIND> tab;
-  __shared__ __attribute__((aligned(16))) f16 a_lds[NT * 16 * kPitch];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  // (tile, row block) of this workgroup: every row block of a tile on the XCD of the tile's index
-  const int L = blockIdx.x, xcd = L % kXcds, s = L / kXcds;
-  const int t0 = kXcds * (s / p.row_blocks) + xcd, rb = s % p.row_blocks;
-  if (t0 >= p.n_tiles) return;
-  const uint32_t e = p.tile_expert[t0];
-  if (e >= (uint64_t)p.experts) return;  // a tile nothing fills: left out
-  if (t0 % NT != 0 && p.tile_expert[t0 - 1] == e) return;  // a tile of a chunk that starts before it
-  const int wend = min((t0 / NT + 1) * NT, p.n_tiles);
-  int nt = 1;
-#pragma unroll
-  for (int i = 1; i < NT; ++i)
-    if (t0 + i < wend && nt == i && p.tile_expert[t0 + i] == e) nt = i + 1;
-  nt = __builtin_amdgcn_readfirstlane(nt);
-
-  {  // the codebooks, read after the K loop's first barrier
-    strata_mv::TableFetch<KIND> tf;
-    strata_mv::fetch_tables<KIND, kThreadsWg>(tf, tid);
-    strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
-  }
+  const int lane = tid & 63;
 
   // the lane's rows and fields
   const int n = lane & 15, g = lane >> 4;
@@ -151,29 +185,26 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
   // the thread's pieces of the activations: (tile, slot, piece) -> global row and LDS place
   const f16* arow[kLoads];
   int adst[kLoads];
-  bool aon[kLoads];
 #pragma unroll
   for (int q = 0; q < kLoads; ++q) {
     const int c = tid + q * kThreadsWg;
     const int i = c / (16 * (kStep / 8)), m = (c / (kStep / 8)) % 16, piece = c % (kStep / 8);
     const int slot = (t0 + i) * 16 + m;
-    aon[q] = i < nt;
-    const uint32_t r = aon[q] ? (p.a_row ? p.a_row[slot] : (uint32_t)slot) : 0u;
+    const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
     arow[q] = p.a + (int64_t)r * p.cols + 8 * piece;
     adst[q] = (i * 16 + m) * kPitch + 8 * piece;
   }
   u32x4 av[kLoads];
 #pragma unroll
-  for (int q = 0; q < kLoads; ++q)
-    if (aon[q]) av[q] = *reinterpret_cast<const u32x4*>(arow[q]);
+  for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q]);
 
   RunPair<KIND> f[2][2];  // [step parity][row group]
   strata_mv::load_fields<KIND>(mat0, off0, o, f[0][0]);
   strata_mv::load_fields<KIND>(mat1, off1, o, f[0][1]);
 
-  f32x4 acc[2][NT];
+  f32x4 acc[2][NTC];
 #pragma unroll
-  for (int i = 0; i < NT; ++i) acc[0][i] = acc[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NTC; ++i) acc[0][i] = acc[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int kb = 0; kb < nsteps; kb += 2) {
 #pragma unroll
@@ -186,52 +217,53 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
         strata_mv::load_fields<KIND>(mat1, off1 + nx, o, f[sp ^ 1][1]);
         __syncthreads();  // every wave has read the last step's activations (and the tables are written)
 #pragma unroll
-        for (int q = 0; q < kLoads; ++q)
-          if (aon[q]) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+        for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
         if (k + 1 < nsteps) {
 #pragma unroll
-          for (int q = 0; q < kLoads; ++q)
-            if (aon[q]) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 1) * kStep);
+          for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 1) * kStep);
         }
         __syncthreads();
 
-        f32x4 part[2][NT];
+        f32x4 part[2][NTC];
 #pragma unroll
-        for (int i = 0; i < NT; ++i) part[0][i] = part[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < NTC; ++i) part[0][i] = part[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
+          f16x8 a8[4][NTC];  // the first two read ahead of the decode, so their latency passes under it
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int i = 0; i < NTC; ++i)
+              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
           uint32_t w0[16], w1[16];
-          strata_mv::decode_run<KIND>(f[sp][0], h, g, w0, tab);
-          fold_run<KIND>(f[sp][0], h, g, w0);
-          strata_mv::decode_run<KIND>(f[sp][1], h, g, w1, tab);
-          fold_run<KIND>(f[sp][1], h, g, w1);
+          decode_folded<KIND>(f[sp][0], h, g, w0, tab);
+          decode_folded<KIND>(f[sp][1], h, g, w1, tab);
+#pragma unroll
+          for (int q = 2; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < NTC; ++i)
+              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[4 * q], w0[4 * q + 1], w0[4 * q + 2], w0[4 * q + 3]});
             const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[4 * q], w1[4 * q + 1], w1[4 * q + 2], w1[4 * q + 3]});
-            const int col = a_col<KIND>(g, h, q);
 #pragma unroll
-            for (int i = 0; i < NT; ++i) {
-              if (i < nt) {
-                const f16x8 a8 = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + col);
-                f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
-                f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
-                p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b0, p0, 0, 0, 0);
-                p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b1, p1, 0, 0, 0);
-              }
+            for (int i = 0; i < NTC; ++i) {
+              f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
+              f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
+              p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b0, p0, 0, 0, 0);
+              p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b1, p1, 0, 0, 0);
             }
           }
         }
         if constexpr (has_step_scale<KIND>()) {
           const float s0 = step_scale<KIND>(f[sp][0]), s1 = step_scale<KIND>(f[sp][1]);
 #pragma unroll
-          for (int i = 0; i < NT; ++i) {
-            if (i < nt) {
+          for (int i = 0; i < NTC; ++i) {
 #pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                acc[0][i][j] = __builtin_fmaf(s0, part[0][i][j], acc[0][i][j]);
-                acc[1][i][j] = __builtin_fmaf(s1, part[1][i][j], acc[1][i][j]);
-              }
+            for (int j = 0; j < 4; ++j) {
+              acc[0][i][j] = __builtin_fmaf(s0, part[0][i][j], acc[0][i][j]);
+              acc[1][i][j] = __builtin_fmaf(s1, part[1][i][j], acc[1][i][j]);
             }
           }
         }
@@ -241,36 +273,72 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
 
   // lane (n, g) holds slots 4g + j of each tile, for rows row0 and row1
 #pragma unroll
-  for (int i = 0; i < NT; ++i) {
-    if (i < nt) {
+  for (int i = 0; i < NTC; ++i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int slot = (t0 + i) * 16 + 4 * g + j;
-        float v0 = acc[0][i][j], v1 = acc[1][i][j];
-        if (p.a_max != nullptr) {
-          const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
-          const int ex = row_exponent(p.a_max[r]);
-          v0 = __builtin_ldexpf(v0, ex);
-          v1 = __builtin_ldexpf(v1, ex);
-        }
-        if constexpr (MODE == PM_C32) {
-          float* c = reinterpret_cast<float*>(p.out) + (int64_t)slot * p.rows;
-          if (row0 < p.rows) c[row0] = v0;
-          if (row1 < p.rows) c[row1] = v1;
-        } else if constexpr (MODE == PM_GLU) {
-          if (row0 < p.rows) store_out<OT>(reinterpret_cast<OT*>(p.out) + (int64_t)slot * p.rows + row0,
-                                           swiglu_f32(v0, v1));
-        } else {
-          const uint32_t pr = p.slot_pair[slot];
-          if (pr != 0xffffffffu) {
-            OT* y = reinterpret_cast<OT*>(p.out) + (int64_t)pr * p.rows;
-            if (row0 < p.rows) store_out<OT>(y + row0, v0);
-            if (row1 < p.rows) store_out<OT>(y + row1, v1);
-          }
+    for (int j = 0; j < 4; ++j) {
+      const int slot = (t0 + i) * 16 + 4 * g + j;
+      float v0 = acc[0][i][j], v1 = acc[1][i][j];
+      if (p.a_max != nullptr) {
+        const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
+        const int ex = row_exponent(p.a_max[r]);
+        v0 = __builtin_ldexpf(v0, ex);
+        v1 = __builtin_ldexpf(v1, ex);
+      }
+      if constexpr (MODE == PM_C32) {
+        float* c = reinterpret_cast<float*>(p.out) + (int64_t)slot * p.rows;
+        if (row0 < p.rows) c[row0] = v0;
+        if (row1 < p.rows) c[row1] = v1;
+      } else if constexpr (MODE == PM_GLU) {
+        if (row0 < p.rows)
+          store_out<OT>(reinterpret_cast<OT*>(p.out) + (int64_t)slot * p.rows + row0, swiglu_f32(v0, v1));
+      } else {
+        const uint32_t pr = p.slot_pair[slot];
+        if (pr != 0xffffffffu) {
+          OT* y = reinterpret_cast<OT*>(p.out) + (int64_t)pr * p.rows;
+          if (row0 < p.rows) store_out<OT>(y + row0, v0);
+          if (row1 < p.rows) store_out<OT>(y + row1, v1);
         }
       }
     }
   }
+}
+
+template <int KIND, int MODE, typename OT, int WAVES, int NT>
+__global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptParams p) {
+  constexpr int kThreadsWg = 64 * WAVES;
+  __shared__ DirectTables<KIND> tab;
+  __shared__ __attribute__((aligned(16))) f16 a_lds[NT * 16 * kPitch];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // (tile, row block) of this workgroup: windows of NT tiles dealt to the XCDs in turn (every row block of a
+  // window's tiles on one XCD), so that the chunks, which start at the windows, spread evenly
+  const int L = blockIdx.x, xcd = L % kXcds, s = L / kXcds;
+  const int per_window = NT * p.row_blocks;
+  const int w = kXcds * (s / per_window) + xcd, j = (s / p.row_blocks) % NT, rb = s % p.row_blocks;
+  const int t0 = w * NT + j;
+  if (t0 >= p.n_tiles) return;
+  const uint32_t e = p.tile_expert[t0];
+  if (e >= (uint64_t)p.experts) return;  // a tile nothing fills: left out
+  if (t0 % NT != 0 && p.tile_expert[t0 - 1] == e) return;  // a tile of a chunk that starts before it
+  const int wend = min((t0 / NT + 1) * NT, p.n_tiles);
+  int nt = 1;
+#pragma unroll
+  for (int i = 1; i < NT; ++i)
+    if (t0 + i < wend && nt == i && p.tile_expert[t0 + i] == e) nt = i + 1;
+  nt = __builtin_amdgcn_readfirstlane(nt);
+
+  {  // the codebooks, read after the K loop's first barrier
+    strata_mv::TableFetch<KIND> tf;
+    strata_mv::fetch_tables<KIND, kThreadsWg>(tf, tid);
+    strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
+  }
+  static_assert(NT == 2, "chunks of one or two tiles");
+  if (nt == 1)
+    run_chunk<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, e, t0, rb, tid, wave);
+  else
+    run_chunk<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, e, t0, rb, tid, wave);
 }
 
 template <int MODE>
@@ -290,7 +358,7 @@ template <int KIND, int MODE, typename OT>
 int launch_prompt(PromptParams& p, hipStream_t s) {
   constexpr int rpw = rows_per_wg<MODE>(kWaves);
   p.row_blocks = (p.rows + rpw - 1) / rpw;
-  const int64_t tiles = (p.n_tiles + kXcds - 1) / kXcds * kXcds;
+  const int64_t tiles = (p.n_tiles + kXcds * kTiles - 1) / (kXcds * kTiles) * (kXcds * kTiles);
   const int64_t grid = tiles * p.row_blocks;
   if (grid <= 0) return STRATA_OK;
   if (grid > 0x7fffffff) return STRATA_ERR_SHAPE;
