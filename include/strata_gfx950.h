@@ -118,6 +118,17 @@ int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t ex
 int strata_rows_to_f16(const void* a, int64_t rows, int64_t cols, int a_dtype, void* out, uint32_t* row_max,
                        void* stream);
 
+/* strata_route_tiles with its workspace in the library's own device memory (a file-scope array of about 1 MB a
+ * GPU, held until the process ends): the call allocates nothing, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. pairs at
+ * most 65536 and experts at most 1024, else STRATA_ERR_SHAPE; STRATA_ERR_LAUNCH if the array's address cannot be
+ * found. The first call on a device looks that address up (with that device current). Every call on one GPU uses
+ * the same array: calls that overlap on one GPU (two streams, two threads) race. The outputs are those of
+ * strata_route_tiles, bit for bit. */
+int strata_route_tiles_noalloc(const uint32_t* idx, int64_t pairs, int64_t k, int64_t experts, int64_t tile,
+                               uint32_t* tile_expert, uint32_t* token, uint32_t* where, uint32_t* slot_pair,
+                               void* stream);
+
 /* c[s, :] = W[tile_expert[s / tile]] . a[s, :] for s < n_tiles * tile; a (n_tiles * tile, cols) in
  * a_dtype (F16 or F32), c (n_tiles * tile, rows) float32. Tiles naming no expert (>= experts) are skipped and
  * their rows of c are left as they were. a_max (F16 only, or NULL): a's rows were scaled by strata_rows_to_f16

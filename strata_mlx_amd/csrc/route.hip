@@ -10,6 +10,8 @@
 //   place  each pair's rank among its block's pairs of the same expert (wave ballots, then the waves
 //          before it), plus its block's offset: the slot; where, token and slot_pair written
 // The tile count is pairs / tile + min(experts, pairs) whatever the routing, as the reference's.
+#include <atomic>
+
 #include "common.h"
 
 namespace {
@@ -105,6 +107,30 @@ __global__ __launch_bounds__(kBlock) void route_place(const uint32_t* idx, int p
   }
 }
 
+// The workspace of strata_route_tiles_noalloc: the library's own device memory, sized for its largest call. Every
+// word the kernels read is written by the same call first (the counts by route_count, the first tiles by
+// route_scan), so the array needs no clearing between calls; calls that overlap on one GPU share it and race.
+constexpr int64_t kScratchPairs = 65536;  // pairs a call takes at most (8192 tokens x top-8)
+constexpr int64_t kScratchExperts = 1024;
+constexpr int64_t kScratchWords = ((kScratchPairs + kBlock - 1) / kBlock) * kScratchExperts + kScratchExperts + 64;
+__device__ __align__(256) uint32_t scratch[kScratchWords];
+
+// scratch's device address on each device, looked up once per device with that device current (in host code the
+// array's name stands in for it and is not a device address)
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_ptr[kMaxDevices];
+
+void* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return nullptr;
+    scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -149,3 +175,14 @@ int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t ex
 }
 
 }  // extern "C"
+
+extern "C" int strata_route_tiles_noalloc(const uint32_t* idx, int64_t pairs, int64_t k, int64_t experts, int64_t tile,
+                                          uint32_t* tile_expert, uint32_t* token, uint32_t* where,
+                                          uint32_t* slot_pair, void* stream) {
+  if (pairs < 0 || k < 1 || experts < 1 || tile < 1 || tile > 1024) return STRATA_ERR_ARG;
+  if (pairs > kScratchPairs || experts > kScratchExperts) return STRATA_ERR_SHAPE;
+  if (strata_route_tiles_workspace(pairs, experts) > kScratchWords * (int64_t)sizeof(uint32_t)) return STRATA_ERR_SHAPE;
+  void* ws = device_scratch();
+  if (ws == nullptr) return STRATA_ERR_LAUNCH;
+  return strata_route_tiles(idx, pairs, k, experts, tile, tile_expert, token, where, slot_pair, ws, stream);
+}

@@ -71,6 +71,10 @@ def test_arguments_are_checked_before_any_launch():
     dn = lib.strata_prompt_down
     assert dn(x3, 1, 4, 64, 256, 1, None, 1, 1, 16, 1, 1, -1, 1, 1, None) == _lib.ERR_ARG  # negative pairs
     assert dn(x3, 1, 4, 64, 256, 1, None, 1, 1, 16, 1, 0, 4, 1, 1, None) == _lib.ERR_ARG  # null idx
+    na = lib.strata_route_tiles_noalloc
+    assert na(1, 65537, 8, 256, 16, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # more pairs than its array takes
+    assert na(1, 4096, 8, 1025, 16, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # more experts
+    assert na(1, 4096, 0, 256, 16, 1, 1, 1, 1, None) == _lib.ERR_ARG
     with pytest.raises(ValueError):
         _lib.check(_lib.ERR_SHAPE, "x")
     with pytest.raises(RuntimeError):
