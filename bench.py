@@ -7,18 +7,23 @@ batch through 16 distinct routed-expert layers (about 1 GB of expert bytes, four
 once as a HIP graph and replayed; each layer is two launches (gate+up writing silu(gate) * up, then down).
 value = algorithmic bytes / time: the distinct experts' packed bytes plus activations in and out.
 
-Beside it, on the same line:
-  decode_t4   the same at 4 tokens (the other batch of the decode workload)
-  prompt      512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, three MFMA
-              grouped products; TFLOPS over the real pairs' 2 * pairs * 3 * 4096 * 1536 flops
-  roofline    the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
-              (HIP events around a graph of those launches only), against 8 TB/s
-  cpu_baseline the oracle's numpy decode + matvec (the reference's CPU path restated) on a few layers
+Beside it, on the same line, the other workloads of the path:
+  decode_t4      the same at 4 tokens
+  speculate      the same layer in Q2_0, 5 rows (1 + 4 draft tokens), 16 layers
+  q4k_matvec     one Q4_K 4096 x 4096 matrix, float32 x, batch 1 (graphs of 64 distinct copies), and its CPU path
+  prompt         512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, the fused
+                 gate/up/SwiGLU and scatter-down MFMA kernels; TFLOPS over the real pairs' 2 * pairs * 3 * H * F
+  dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K, o Q8_0, the shared
+                 expert's Q4_K gate / up 1536 x 4096 and down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16
+                 token each (graphs over copies, at least 1 GB a graph)
+  prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
+                 the dense layers as tile products, TFLOPS
+  roofline       the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
+                 (HIP events around a graph of those launches only), against 8 TB/s
+  cpu_baseline   the oracle's numpy decode of the touched experts (one thread) + float32 matvecs (BLAS on the
+                 host's cores) on a few layers of the headline workload; q4k_matvec carries its own
 
---dense prints only the dense half of a decode token of the mixed model instead (one JSON line): q, k, v 4096 x
-4096 Q6_K, o 4096 x 4096 Q8_0, the shared expert's gate / up 1536 x 4096 and down 4096 x 1536 Q4_K, lm_head
-151936 x 4096 Q6_K (510.5 MB), each through `window_matvec` at one token, as graphs over copies of each
-weight (at least 1 GB a graph, past the MALL).
+--dense prints only dense_decode as its own line.
 """
 
 import argparse
@@ -34,6 +39,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 E, H, F, K = 256, 4096, 1536, 8
+VOCAB = 151936
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
@@ -47,6 +53,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prompt", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline, decode_t4, roofline and prompt")
     ap.add_argument("--dense", action="store_true", help="only the dense half of a mixed-model decode token")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 512 MiB with torch's copy kernel three times: the known-size reference that "
@@ -82,14 +89,14 @@ def time_graph(graph, steps, warmup):
     return start.elapsed_time(end) / 1e3  # seconds
 
 
-def decode_layers(B, synth, dev, layers):
+def decode_layers(B, synth, dev, layers, kind="IQ3_S", seed=0):
     g = torch.Generator(device=dev)
-    g.manual_seed(0)
+    g.manual_seed(seed)
     out = []
     for _ in range(layers):
-        mats = [synth.random_stack("IQ3_S", E * r * c, dev, g) for r, c in ((F, H), (F, H), (H, F))]
-        out.append((B.BlockSwitchLinear(mats[0], "IQ3_S", (E, F, H)), B.BlockSwitchLinear(mats[1], "IQ3_S", (E, F, H)),
-                    B.BlockSwitchLinear(mats[2], "IQ3_S", (E, H, F))))
+        mats = [synth.random_stack(kind, E * r * c, dev, g) for r, c in ((F, H), (F, H), (H, F))]
+        out.append((B.BlockSwitchLinear(mats[0], kind, (E, F, H)), B.BlockSwitchLinear(mats[1], kind, (E, F, H)),
+                    B.BlockSwitchLinear(mats[2], kind, (E, H, F))))
     return out
 
 
@@ -98,7 +105,7 @@ def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
     routes = [synth.zipf_routing(tokens, E, K, rng)[0] for _ in lins]
     idx = [torch.from_numpy(r).to(torch.int32).to(dev) for r in routes]
     x = (torch.randn((tokens, H), device=dev)).half()
-    mat_bytes = F * H // 256 * 110
+    mat_bytes = lins[0][0].blocks.numel() // E
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):  # one eager pass first: the library's lazy state, torch's allocator
@@ -189,10 +196,28 @@ def dense_bench(B, synth, dev, steps, warmup):
             "data": "synthetic (random blocks)", "layers": out}
 
 
+def host_cpu():
+    """(the host's cores as this process sees them, the threads BLAS is given, the CPU model)."""
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = int(os.environ.get("OMP_NUM_THREADS", cores) or cores)
+    threads = max(1, min(threads, cores))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, threads, model
+
+
 def cpu_baseline(lins, routes, tokens, budget_s=15.0, max_layers=4):
-    """The oracle's numpy decode of the touched experts and their matvecs, one thread, layer by layer until about
-    budget_s of CPU work. The experts' bytes are copied to the host first, untimed: the CPU path reads them from
-    memory. Returns (layers, algorithmic bytes, seconds)."""
+    """The reference's CPU path restated (the oracle): numpy decode of the touched experts (one thread, as numpy
+    decodes) and their float32 matvecs (BLAS on the host's cores), layer by layer until about budget_s of CPU work.
+    The experts' bytes are copied to the host first, untimed: the CPU path reads them from memory. Returns (layers,
+    algorithmic bytes, seconds, BLAS threads)."""
     from threadpoolctl import threadpool_limits
 
     from oracle import blocks as O
@@ -200,7 +225,8 @@ def cpu_baseline(lins, routes, tokens, budget_s=15.0, max_layers=4):
     mat_bytes = F * H // 256 * 110
     done, secs, layers = 0, 0.0, 0
     x = np.random.default_rng(5).standard_normal((tokens, H)).astype(np.float16)
-    with threadpool_limits(limits=1):
+    _, threads, _ = host_cpu()
+    with threadpool_limits(limits=threads):
         for (gate, up, down), r in zip(lins, routes):
             used = [int(e) for e in np.unique(r)]
             host = {n: {e: lin.blocks[e * mat_bytes:(e + 1) * mat_bytes].cpu().numpy() for e in used}
@@ -219,7 +245,92 @@ def cpu_baseline(lins, routes, tokens, budget_s=15.0, max_layers=4):
             done += len(used) * 3 * mat_bytes + x.nbytes + 2 * len(flat) * F * 2 + len(flat) * H * 2
             if secs > budget_s or layers >= max_layers:
                 break
-    return layers, done, secs
+    return layers, done, secs, threads
+
+
+def q4k_bench(B, synth, dev, steps, warmup, copies=64):
+    """One Q4_K 4096 x 4096 matrix times float32 x, batch 1: graphs over `copies` distinct matrices (604 MB, past
+    the MALL). Returns the sub-object, with the CPU path (the oracle's to_affine-style decode, then x @ W.T) timed on
+    the host beside it."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import blocks as O
+
+    rows = cols = 4096
+    nbytes = rows * cols // 256 * 144
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    mats = [synth.random_stack("Q4_K", rows * cols, dev, g) for _ in range(copies)]
+    x = torch.randn((1, cols), device=dev)
+    B.window_matvec(mats[0], "Q4_K", rows, cols, x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for m in mats:
+            B.window_matvec(m, "Q4_K", rows, cols, x)
+    t = time_graph(graph, steps, warmup) / steps / copies
+    moved = nbytes + cols * 4 + rows * 4
+    host = mats[0].cpu().numpy()
+    xh = x.cpu().numpy()
+    cores, threads, model = host_cpu()
+    reps, secs = 0, 0.0
+    with threadpool_limits(limits=threads):
+        while secs < 5.0 and reps < 50:
+            t0 = time.perf_counter()
+            w = O.dequantize(host, "Q4_K", (rows, cols))
+            xh @ w.T
+            secs += time.perf_counter() - t0
+            reps += 1
+    del mats
+    torch.cuda.empty_cache()
+    return {"workload": "Q4_K 4096x4096 matvec, float32 x, batch 1", "us_per_matvec": round(t * 1e6, 2),
+            "gbs": round(moved / t / 1e9, 1), "hbm_frac": round(moved / t / 1e9 / HBM_PEAK_GBS, 4),
+            "cpu": {"us_per_matvec": round(secs / reps * 1e6, 1), "gbs": round(moved * reps / secs / 1e9, 4),
+                    "cores": threads, "kind": "port",
+                    "sample": f"{reps} matvecs: numpy decode (one thread) + x @ W.T (BLAS, {threads} threads)"}}
+
+
+def prefill_bench(B, D, synth, dev, lins, steps, warmup, rng, tokens=2048):
+    """A 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts of `lins` (Zipf top-8) through
+    the tiles, and the dense layers (q, k, v Q6_K, o Q8_0, the shared expert's Q4_K gate, up, down) as tile products
+    of the whole chunk. Returns TFLOPS over the real products' flops, each part and all."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    dense = [D.BlockLinear(synth.random_stack(kind, r * c, dev, g), kind, (r, c))
+             for kind, r, c in (("Q6_K", H, H), ("Q6_K", H, H), ("Q6_K", H, H), ("Q8_0", H, H), ("Q4_K", F, H),
+                                ("Q4_K", F, H), ("Q4_K", H, F))]
+    idx = [torch.from_numpy(synth.zipf_routing(tokens, E, K, rng)[0]).to(torch.int32).to(dev) for _ in lins]
+    x = torch.randn((tokens, H), device=dev).to(torch.bfloat16)
+    xf = torch.randn((tokens, F), device=dev).to(torch.bfloat16)
+
+    def routed():
+        for (gate, up, down), ix in zip(lins, idx):
+            B._tiled_glu(x, ix, up, gate, down)
+
+    def dense_all():
+        for lin in dense:
+            lin(xf if lin.input_dims == F else x)
+
+    out = {}
+    for name, fn, flops in (("routed", routed, 2.0 * tokens * K * 3 * H * F * len(lins)),
+                            ("dense", dense_all, sum(2.0 * tokens * lin.output_dims * lin.input_dims for lin in dense))):
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        t = time_graph(graph, steps, warmup) / steps
+        out[name] = {"tflops": round(flops / t / 1e12, 2), "ms": round(t * 1e3, 4),
+                     "layers": len(lins) if name == "routed" else len(dense)}
+        out[name]["_flops"] = flops
+    fl = out["routed"]["_flops"] / len(lins) + out["dense"]["_flops"]
+    ms = out["routed"]["ms"] / len(lins) + out["dense"]["ms"]
+    for v in out.values():
+        v.pop("_flops")
+    out.update({"workload": "2048-token prefill, bf16: routed IQ3_S 256 experts top-8 (one layer) + dense q/k/v "
+                            "Q6_K, o Q8_0, shared expert Q4_K", "tflops": round(fl / ms / 1e9, 2),
+                "ms_per_layer": round(ms, 4), "mfma_peak_frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)})
+    return out
 
 
 def main():
@@ -273,16 +384,38 @@ def main():
                      "kernel": "direct_decode_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
                      "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
     }
+    if not args.no_extra:
+        note("speculative verify, Q2_0, 5 rows")
+        q2 = decode_layers(B, synth, dev, args.layers, "Q2_0", seed=7)
+        gq, msq, _, (gq_bytes, gq_s), _ = decode_bench(B, synth, dev, q2, 5, args.steps, args.warmup, rng)
+        result["speculate"] = {"workload": "Q2_0 routed decode, 256 experts top-8, 5 rows (1 + 4 draft), 16 layers",
+                               "gbs": round(gq, 1), "ms_per_step": round(msq, 4), "hbm_frac": round(gq / HBM_PEAK_GBS, 4),
+                               "gate_up_kernel_gbs": round(gq_bytes / gq_s / 1e9, 1)}
+        del q2
+        torch.cuda.empty_cache()
+        note("Q4_K 4096 x 4096, float32 x")
+        result["q4k_matvec"] = q4k_bench(B, synth, dev, max(2, args.steps // 5), 2)
     if not args.no_prompt:
         note("prompt chunk")
         result["prompt"] = prompt_bench(B, synth, dev, max(2, args.steps // 10), 2, rng)
+    if not args.no_extra:
+        note("dense half of a decode token")
+        dd = dense_bench(B, synth, dev, max(2, args.steps // 5), 2)
+        result["dense_decode"] = {k: dd[k] for k in ("value", "unit", "us_per_token", "bytes_per_token", "hbm_frac")}
+        result["dense_decode"]["layers"] = {n: {k: v[k] for k in ("kind", "us", "hbm_frac")} for n, v in dd["layers"].items()}
+        note("2048-token prefill")
+        from strata_mlx_amd import dense as D
+        result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng)
     if not args.no_cpu_baseline:
         note("cpu baseline")
-        layers, done, secs = cpu_baseline(lins, routes, args.tokens)
-        result["cpu_baseline"] = {"value": round(done / secs / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-                                  "sample": f"{layers} layers at batch {args.tokens}: numpy decode of the touched "
-                                            f"experts + float32 matvecs + SwiGLU (oracle/blocks.py), one thread",
-                                  "seconds": round(secs, 2)}
+        layers, done, secs, threads = cpu_baseline(lins, routes, args.tokens)
+        cores, _, model = host_cpu()
+        result["cpu_baseline"] = {"value": round(done / secs / 1e9, 4), "unit": "GB/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"{layers} layers of the headline workload at batch {args.tokens}: numpy "
+                                            f"decode of the touched experts (one thread) + float32 matvecs (BLAS, "
+                                            f"{threads} threads) + SwiGLU (oracle/blocks.py)",
+                                  "seconds": round(secs, 2), "host_cores": cores, "cpu_model": model}
     print(json.dumps(result))
 
 

@@ -270,6 +270,11 @@ def q3k_planes_dequantize(planes: dict, rows: int, cols: int, dtype: torch.dtype
 # their two inputs; with those sums in a float16 table a code byte costs two table reads. float16 only.
 
 LOOKUP_FROM = 1  # (token, expert) pairs from which Q2_0 experts over float16 go this way (blocks.py:711)
+# switch_glu sends Q2_0 experts over float16 to the table of sums when True, as the reference's dispatch does
+# (blocks.py:963-964); its sums are rounded to float16 (about 2e-3 relative L2 off the exact products at a decode
+# layer's shape). By default they take the register-decode kernels instead: exact products and float32 sums (within
+# 1e-3), and one launch fewer a layer.
+LOOKUP_GLU = False
 LOOKUP_MAX_COLS = 4096  # a token's table, 16 * cols bytes, is held in LDS
 
 
@@ -395,9 +400,10 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, ga
     The argument order is the reference's (x, indices, up, gate, down); strata_mlx/blocks.py:958-986.
 
     Decode windows take the matvec kernels: gate and up in one launch reading x once and writing silu(gate) * up
-    (rounded as mlx-lm rounds it), then down on that. Q2_0 stacks over float16 take the table of sums, as the
-    reference's do (blocks.py:963-964). Prompt chunks (from TILES_FROM pairs) take the tiles: the pairs sorted by
-    expert on the GPU, weights decoded into LDS and multiplied on MFMA."""
+    (rounded as mlx-lm rounds it), then down on that; Q2_0 stacks over float16 too, unless LOOKUP_GLU sends them to
+    the table of sums as the reference's dispatch does (blocks.py:963-964). Prompt chunks (from TILES_FROM pairs) take
+    the tiles: the pairs sorted by expert on the GPU, gate and up with the SwiGLU in one MFMA launch, down written
+    straight to the pairs."""
     indices = torch.as_tensor(indices, device=x.device)
     k = indices.shape[-1] if indices.ndim else 1
     flat = indices.reshape(-1)
@@ -405,7 +411,7 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, ga
     if flat.numel() >= TILES_FROM and all(tileable(lin.kind, lin.output_dims, lin.input_dims)
                                           for lin in (up, gate, down)):
         return _tiled_glu(x, indices, up, gate, down)
-    if flat.numel() >= LOOKUP_FROM and all(lookable(lin, x.dtype) for lin in (up, gate, down)):
+    if LOOKUP_GLU and flat.numel() >= LOOKUP_FROM and all(lookable(lin, x.dtype) for lin in (up, gate, down)):
         return _lookup_glu(x, indices, up, gate, down)
     if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) == (up.kind, up.output_dims, up.input_dims,
                                                                              up.num_experts):

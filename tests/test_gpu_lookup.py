@@ -82,8 +82,17 @@ def test_the_table_built_in_down_gives_the_bits_of_its_own_launch(gpu, pairs, ro
     assert torch.equal(got, B.lookup_matvec(down, idx, B.lookup_table_glu(gate, up), 1))
 
 
-def test_a_layer_through_switch_glu_is_the_product(gpu):
-    """Config 3's shape: 5 tokens x top-8 over Q2_0 gate/up 1536 x 4096, down 4096 x 1536."""
+@pytest.fixture
+def lookup_dispatch():
+    old = B.LOOKUP_GLU
+    B.LOOKUP_GLU = True  # switch_glu takes the table of sums for Q2_0 over float16, as the reference's does
+    yield
+    B.LOOKUP_GLU = old
+
+
+def test_a_layer_through_switch_glu_is_the_product(gpu, lookup_dispatch):
+    """Config 3's shape: 5 tokens x top-8 over Q2_0 gate/up 1536 x 4096, down 4096 x 1536, through the table path
+    (float16 sums: 2e-3 relative L2)."""
     rng = np.random.default_rng(3)
     E, H, F, k, tokens = 16, 4096, 1536, 8, 5
     mats = {n: O.random_blocks("Q2_0", E * r * c // 64, rng, scale="normal")
