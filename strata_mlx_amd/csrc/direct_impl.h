@@ -1296,6 +1296,12 @@ int launch_direct(MatvecParams& p, bool one_token, int grid_y, int grid_z, hipSt
   return STRATA_ERR_SHAPE;
 }
 
+}  // namespace strata_mv
+
+#include "routed_impl.h"
+
+namespace strata_mv {
+
 // The float16 fast paths where they apply (a type of FastTraits, float16 in and out, rows contiguous): the
 // direct kernel, else the persistent wave kernel, else the staged fast kernel; other cases the generic kernels.
 template <int KIND>
@@ -1327,9 +1333,11 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
                                                                      : (glu ? p.pairs <= 16
                                                                             : p.pairs <= p.share || p.pairs <= 64));
       if (p.glu_out != nullptr) {
+        if (!glu && grid_z == 2 && routed_glu_takes<KIND>(p)) return launch_routed_glu<KIND>(p, s);
         if (!direct_takes(p) || glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }
+      if (!glu && grid_z == 1 && routed_down_takes<KIND>(p)) return launch_routed_down<KIND>(p, s);
       // the same for the 8-lane rows against two tokens a pass on 32-lane rows (four tokens: 2283 against 2047)
       if (!glu && one && odd_takes<KIND>(p)) return launch_direct_odd<KIND>(p, grid_y, grid_z, s);
       if (direct_takes(p)) {

@@ -1,0 +1,96 @@
+"""The persistent gate/up kernel of one token (IQ3_S rows of 4096 inputs, routed_glu_kernel) at the unit counts
+that pick each of its forms: one to four units a wave, and more units than one round of resident waves holds.
+Against the oracle: g and u at 1e-3 relative L2 against float64 products of the oracle's weights, h within one
+float16 step of the SwiGLU of the kernel's own g and u (strata_mlx/blocks.py:222-236), NaN rows for a pair naming
+no expert, and a pair repeating an expert equal to the first pair naming it."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import blocks as O
+from strata_mlx_amd import blocks as B
+from strata_mlx_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+H, REL = 4096, 1e-3
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return np.linalg.norm(got - want) / np.linalg.norm(want)
+
+
+@pytest.fixture(scope="module")
+def stacks(gpu):
+    experts, rows = 12, 1536
+    g = torch.Generator(device=gpu).manual_seed(31)
+    out = {}
+    for name in ("gate", "up"):
+        blocks = synth.random_stack("IQ3_S", experts * rows * H, gpu, g)
+        out[name] = (blocks, B.row_bytes("IQ3_S", H))
+    return out, experts, rows
+
+
+# (pairs, rows): units = pairs * rows; 4096 waves are resident at once on 256 CUs
+@pytest.mark.parametrize("pairs,rows", [(1, 64), (3, 1536), (8, 1536), (10, 1536), (24, 1536), (5, 200)])
+def test_one_token_gate_up(gpu, stacks, pairs, rows):
+    (gate_b, rb), (up_b, _) = stacks[0]["gate"], stacks[0]["up"]
+    experts, all_rows = stacks[1], stacks[2]
+    # the first `rows` rows of each expert: a stack of `experts` matrices of `rows` rows
+    gate_s = gate_b.reshape(experts, all_rows, rb)[:, :rows].contiguous()
+    up_s = up_b.reshape(experts, all_rows, rb)[:, :rows].contiguous()
+    gate = B.BlockSwitchLinear(gate_s, "IQ3_S", (experts, rows, H))
+    up = B.BlockSwitchLinear(up_s, "IQ3_S", (experts, rows, H))
+    rng = np.random.default_rng(pairs * 1000 + rows)
+    idx = rng.integers(0, experts, pairs).astype(np.int32)
+    if pairs >= 3:
+        idx[1] = experts + 5  # names no expert
+        idx[2] = idx[0]       # repeats the first pair's expert
+    x = (rng.standard_normal((1, H)) / 64).astype(np.float16)
+    xs, ix = torch.from_numpy(x).to(gpu), torch.from_numpy(idx).to(gpu)
+    g, u, h = B.gate_up_swiglu(gate, up, xs, ix, pairs)
+    torch.cuda.synchronize()
+    gk, uk, hk = (t.cpu().numpy() for t in (g, u, h))
+    ok = idx < experts
+    assert np.isnan(gk[~ok]).all() and np.isnan(uk[~ok]).all() and np.isnan(hk[~ok]).all()
+    if pairs >= 3:
+        assert np.array_equal(hk[2], hk[0]) and np.array_equal(gk[2], gk[0])
+    gw = gate_s.cpu().numpy().reshape(experts, -1)
+    uw = up_s.cpu().numpy().reshape(experts, -1)
+    xd = x.astype(np.float64)[0]
+    for p in np.nonzero(ok)[0]:
+        e = idx[p]
+        wg = O.dequantize(gw[e], "IQ3_S", (rows, H)).astype(np.float64)
+        wu = O.dequantize(uw[e], "IQ3_S", (rows, H)).astype(np.float64)
+        assert rel_l2(gk[p], wg @ xd) <= REL and rel_l2(uk[p], wu @ xd) <= REL
+    want_h = O.swiglu_rounded(gk[ok], uk[ok], np.float16)
+    steps = np.abs(hk[ok].astype(np.float64) - want_h.astype(np.float64)) / np.maximum(
+        np.spacing(np.abs(want_h.astype(np.float16))).astype(np.float64), 2.0 ** -24)
+    assert steps.max() <= 1.0
+
+
+# (pairs, share, rows, cols): the routed one-matrix kernel (routed_down_kernel) at both row widths it takes, one and
+# two units a wave (more units than 4096 waves), rows not a multiple of eight, tokens shared by several pairs
+@pytest.mark.parametrize("pairs,share,rows,cols", [(8, 1, 4096, 1536), (12, 1, 4096, 1536), (6, 3, 1000, 1536),
+                                                    (4, 1, 2048, 2560), (9, 9, 3000, 2560)])
+def test_routed_down(gpu, pairs, share, rows, cols):
+    experts = 6
+    g = torch.Generator(device=gpu).manual_seed(rows + cols)
+    blocks = synth.random_stack("IQ3_S", experts * rows * cols, gpu, g)
+    lin = B.BlockSwitchLinear(blocks, "IQ3_S", (experts, rows, cols))
+    rng = np.random.default_rng(pairs * 7 + rows)
+    idx = rng.integers(0, experts, pairs).astype(np.int32)
+    idx[1] = experts  # names no expert
+    x = (rng.standard_normal((pairs // share, cols)) / 8).astype(np.float16)
+    y = B.expert_matvec(lin, torch.from_numpy(idx).to(gpu), torch.from_numpy(x).to(gpu), share)
+    torch.cuda.synchronize()
+    yk = y.float().cpu().numpy()
+    assert np.isnan(yk[1]).all()
+    raw = blocks.cpu().numpy().reshape(experts, -1)
+    for p in range(pairs):
+        if p == 1:
+            continue
+        w = O.dequantize(raw[idx[p]], "IQ3_S", (rows, cols)).astype(np.float64)
+        assert rel_l2(yk[p], w @ x[p // share].astype(np.float64)) <= REL
