@@ -61,7 +61,7 @@ def parse():
     return ap.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "direct_decode_gate_up_iq3s_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "routed_glu_iq3s_traffic.md")
 
 
 def measured_traffic():
@@ -381,7 +381,7 @@ def main():
                       "gate_up_kernel_gbs": round(gu4_bytes / gu4_s / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "direct_decode_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
+                     "kernel": "routed_glu_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
                      "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
     }
     if not args.no_extra:
