@@ -85,7 +85,8 @@ class BlockSwitchLinear:
         self.per_row = per_row  # accepted for the reference's signature; the kernel sets its own split
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor, sorted_indices: bool = False) -> torch.Tensor:
-        """x (..., 1, in), one row to each index or to each run of the last axis of `indices`."""
+        """The routed products for `indices`: x is (..., 1, in); every index multiplies the row of x it belongs to
+        (one row per index, or one row shared by the k indices of a token). Returns (..., k, 1, out)."""
         indices = torch.as_tensor(indices, device=x.device)
         batch, k = tuple(x.shape[:-2]), (indices.shape[-1] if indices.ndim else 1)
         ishape = tuple(indices.shape)
@@ -279,7 +280,8 @@ LOOKUP_MAX_COLS = 4096  # a token's table, 16 * cols bytes, is held in LDS
 
 
 def _threads_per_row(runs: int) -> int:
-    """As many as divide a row evenly and leave each at least four runs (strata_mlx/blocks.py:303-308)."""
+    """Lanes the lookup kernels give a row: doubled while the row's runs still split evenly and every lane keeps
+    four runs or more, at most 32 (the rule of strata_mlx/blocks.py:303-308, which fixes the summation order)."""
     p = 1
     while p < 32 and runs % (2 * p) == 0 and runs // (2 * p) >= 4:
         p *= 2
@@ -302,7 +304,8 @@ def lookable(lin, dtype: torch.dtype) -> bool:
 
 
 def lookup_table(x: torch.Tensor) -> torch.Tensor:
-    """x (n, cols) float16 -> (n, cols / 2, 16): for every two inputs, the sums two weights can make of them.
+    """The Q2_0 table of sums: for each token of x (n, cols) float16 and each pair of its inputs (a, b), the 16
+    values (c & 3 - 1) a + (c >> 2 - 1) b, one for each nibble c of two 2-bit codes: (n, cols / 2, 16) float16.
     strata_mlx/blocks.py:768-777."""
     if x.dtype != torch.float16:
         raise ValueError("lookup_table takes float16 activations")
@@ -345,8 +348,9 @@ def _lookup(lins: tuple, idx: torch.Tensor, table: torch.Tensor, share: int) -> 
 
 
 def lookup_matvec(lin, idx: torch.Tensor, table: torch.Tensor, share: int) -> torch.Tensor:
-    """out[pair] = W[idx[pair]] . x[pair / share], x given as its `lookup_table`. Returns (pairs, rows) float16.
-    strata_mlx/blocks.py:792-812."""
+    """The routed Q2_0 product read through a table of sums: row r of pair p is the sum, over the row's code
+    nibbles, of the entries of token p / share's `lookup_table` that they select, times each block's d.
+    (pairs, rows) float16. strata_mlx/blocks.py:792-812."""
     return _lookup((lin,), idx, table, share)[0]
 
 
@@ -425,7 +429,8 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, up: BlockSwitchLinear, ga
 
 
 class BlockSwitchGLU:
-    """A layer's routed experts, called like mlx-lm's `SwitchGLU`; strata_mlx/blocks.py:989-996."""
+    """gate, up and down of one layer's expert stacks behind mlx-lm's `SwitchGLU` call (x, indices) -> y, which
+    `switch_glu` computes; strata_mlx/blocks.py:989-996."""
 
     def __init__(self, gate: BlockSwitchLinear, up: BlockSwitchLinear, down: BlockSwitchLinear):
         self.gate_proj, self.up_proj, self.down_proj = gate, up, down
@@ -438,7 +443,8 @@ ROWS_TILE, COLS_TILE = 64, 64  # what a tile takes (strata_mlx/blocks.py:581, 62
 
 
 def tileable(kind: str, rows: int, cols: int) -> bool:
-    """Whether `tile_matmul` takes a stack of such layers; strata_mlx/blocks.py:629-631."""
+    """True when rows and cols are whole 64 x 64 tiles, cols whole blocks of the type, and the type has a decoder
+    here: the stacks `tile_matmul` multiplies (strata_mlx/blocks.py:629-631)."""
     per_block = {**BLOCK, **DENSE}[kind][0]
     return rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % per_block == 0 and kind not in NO_GRID
 
