@@ -1,6 +1,6 @@
-// Routed gate and up with the SwiGLU for one token, on IQ3_S rows of 4096 inputs: the decode matvec of a
-// mixture-of-experts layer at batch one (strata_mlx/blocks.py:958-975 with the SwiGLU of its down call,
-// :222-236), as one persistent launch.
+// Routed gate and up with the SwiGLU, and the routed one-matrix product (down), in IQ3_S and Q2_0 for decode:
+// the matvecs of a mixture-of-experts layer at a few tokens (strata_mlx/blocks.py:958-975 with the SwiGLU of its
+// down call, :222-236), each as one persistent launch.
 //
 // What a launch of direct_decode_kernel spends at this shape is mostly fixed cost: a chain of dependent loads
 // before the first row byte is asked for (the parameters, the pair's expert, the mode's branches), a prologue and
@@ -26,6 +26,12 @@
 //
 // Lane j of a wave holds run pair j of a row (64 weights, the same 128 bytes of the token for every unit); the
 // gate row's partial sums and the up row's meet in one exchange of halves and then within the halves.
+//
+// Several tokens (pairs / share of them, up to 8): every pair is its own unit, and the tokens sit in LDS beside
+// the codebook; a unit reads its token's 128 bytes a lane from there. Units run row by row over all pairs, so the
+// pairs naming one expert read each of its rows at about the same time, and the second read finds the bytes in a
+// cache. Q2_0 takes the same kernels with a 256-entry table of a code byte's four weights (c - 1) in place of the
+// codebook, and d for a lane's block.
 #pragma once
 // Included by direct_impl.h ahead of the dispatch (it uses that file's fields, offsets and reductions).
 
@@ -34,89 +40,146 @@ namespace strata_mv {
 constexpr int kGluThreads = 1024;  // sixteen waves a workgroup, one workgroup a CU
 constexpr int kGluWaves = kGluThreads / 64;
 constexpr int kGluGroupsPerCU = 1;
-constexpr int kGluMaxUnits = 4;     // units a wave (straight-line code); more units: more waves
-constexpr int kGluEntries = 8192;   // 512 grid entries x 16 sign nibbles
+constexpr int kGluMaxUnits = 16;   // units a wave (straight-line code); more units: more waves
+constexpr int kGluMaxTokens = 8;   // tokens in LDS
+
+// What a type brings to these kernels: its LDS table (built by the workgroup), the fields of a lane's run pair
+// (64 weights), their loads and the lane's share of a row's sum.
+template <int KIND>
+struct Routed;
+
+template <>
+struct Routed<K_IQ3_S> {
+  static constexpr int kEntries = 8192;  // 512 grid entries x 16 sign nibbles
+  typedef RunPair<K_IQ3_S> Fields;
+  // the codebook entry thread tid expands (asked for before anything else)
+  static __device__ __forceinline__ uint64_t fetch(int tid) { return kIq3sHalfGrid.v[tid & 511]; }
+  // entry s << 9 | g: grid entry g under sign nibble s (bit b flips weight b); thread tid writes half the nibbles
+  // of entry tid % 512
+  static __device__ __forceinline__ void fill(u32x2* tab, int tid, uint64_t entry) {
+    const uint32_t lo32 = (uint32_t)entry, hi32 = (uint32_t)(entry >> 32);
+    const int half = (tid >> 9) & 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s = 8 * half + i;
+      const uint32_t m0 = ((i & 1) ? 0x8000u : 0u) | ((i & 2) ? 0x80000000u : 0u);
+      const uint32_t m1 = ((i & 4) ? 0x8000u : 0u) | (half ? 0x80000000u : 0u);
+      tab[s * 512 + (tid & 511)] = u32x2{lo32 ^ m0, hi32 ^ m1};
+    }
+  }
+  // run pair j of the row at `row` (d @0, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106 of each 110-byte
+  // block); the loads take the row as a scalar base and a 32-bit lane offset
+  static __device__ __forceinline__ void load(const uint8_t* row, int j, Fields& f) {
+    const uint32_t b = (uint32_t)(j >> 2) * 110, jj = (uint32_t)j & 3;
+    f.d = load_at<uint16_t>(row, b);
+    f.qs = load_at<u32x4>(row + 2, b + 16 * jj);
+    f.qh = load_at<uint16_t>(row + 66, b + 2 * jj);
+    f.sg = load_at<u32x2>(row + 74, b + 8 * jj);
+    f.sc = load_at<uint16_t>(row + 106, b + 2 * (jj >> 1));
+  }
+  // Run h (0, 1): its 32 weights from the signed codebook, times 32 activations (16 packed pairs). Group l's
+  // word: the index byte qs[l] low, the ninth bit and the sign nibble of group l high. The ninth bits of the even
+  // groups (bits 0, 2, 4, 6 of the run's qh byte) go to bit 0 of bytes 0..3 by one multiply (the products' other
+  // bits never reach bits 0, 8, 16, 24), the sign nibbles of the even groups are the low nibbles of the run's
+  // four sign bytes; the odd groups take bits 1, 3, 5, 7 and the high nibbles.
+  static __device__ __forceinline__ float run(const Fields& f, int h, const uint32_t* x, const u32x2* tab) {
+    const uint32_t q0 = f.qs[2 * h], q1 = f.qs[2 * h + 1];
+    const uint32_t hb = (uint32_t)f.qh >> (8 * h);
+    const uint32_t sg = f.sg[h];
+    const uint32_t he = (((hb & 0x55u) * 0x41041u) & 0x01010101u) | ((sg & 0x0F0F0F0Fu) << 1);
+    const uint32_t ho = ((((hb >> 1) & 0x55u) * 0x41041u) & 0x01010101u) | ((sg >> 3) & 0x1E1E1E1Eu);
+    const uint32_t w02 = __builtin_amdgcn_perm(he, q0, 0x05020400u), w13 = __builtin_amdgcn_perm(ho, q0, 0x05030401u);
+    const uint32_t w46 = __builtin_amdgcn_perm(he, q1, 0x07020600u), w57 = __builtin_amdgcn_perm(ho, q1, 0x07030601u);
+    const uint32_t three = 3;
+    const uint32_t a[8] = {word_shl<0>(w02, three), word_shl<0>(w13, three), word_shl<1>(w02, three),
+                           word_shl<1>(w13, three), word_shl<0>(w46, three), word_shl<0>(w57, three),
+                           word_shl<1>(w46, three), word_shl<1>(w57, three)};
+    uint32_t w[16];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const u32x2 v = lds_entry(tab, a[l]);
+      w[2 * l] = v[0];
+      w[2 * l + 1] = v[1];
+    }
+    return dot16x2(w, x + 16 * h);
+  }
+  // lane j's share of a row: its two runs, each times its scale d (1 + 2 s)
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const u32x2* tab) {
+    const float d = half_bits(f.d);
+    const uint32_t sc = (uint32_t)f.sc >> (8 * (j & 1));
+    const float s0 = d * (float)(1 + 2 * (sc & 15u)), s1 = d * (float)(1 + 2 * ((sc >> 4) & 15u));
+    return s0 * run(f, 0, x, tab) + s1 * run(f, 1, x, tab);
+  }
+};
+
+template <>
+struct Routed<K_Q2_0> {
+  static constexpr int kEntries = 256;  // a code byte's four weights c - 1 as float16
+  typedef RunPair<K_Q2_0> Fields;
+  static __device__ __forceinline__ uint64_t fetch(int) { return 0; }
+  static __device__ __forceinline__ void fill(u32x2* tab, int tid, uint64_t) {
+    if (tid < 256) {
+      const uint32_t b = (uint32_t)tid;
+      tab[tid] = u32x2{pack_h2((float)(b & 3) - 1.0f, (float)((b >> 2) & 3) - 1.0f),
+                       pack_h2((float)((b >> 4) & 3) - 1.0f, (float)(b >> 6) - 1.0f)};
+    }
+  }
+  // run pair j = block j of the row (d @0, qs[16] @2 of each 18-byte block; weight k in bits 2 (k % 4) of byte
+  // k / 4, strata_mlx/blocks.py:58-68)
+  static __device__ __forceinline__ void load(const uint8_t* row, int j, Fields& f) {
+    const uint32_t b = (uint32_t)j * 18;
+    f.d = load_at<uint16_t>(row, b);
+    f.qs = load_at<u32x4>(row + 2, b);
+  }
+  static __device__ __forceinline__ float run(const Fields& f, int h, const uint32_t* x, const u32x2* tab) {
+    const uint32_t q0 = f.qs[2 * h], q1 = f.qs[2 * h + 1];
+    const uint32_t three = 3;
+    const uint32_t a[8] = {byte_shl<0>(q0, three), byte_shl<1>(q0, three), byte_shl<2>(q0, three),
+                           byte_shl<3>(q0, three), byte_shl<0>(q1, three), byte_shl<1>(q1, three),
+                           byte_shl<2>(q1, three), byte_shl<3>(q1, three)};
+    uint32_t w[16];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const u32x2 v = lds_entry(tab, a[l]);
+      w[2 * l] = v[0];
+      w[2 * l + 1] = v[1];
+    }
+    return dot16x2(w, x + 16 * h);
+  }
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int, const uint32_t* x, const u32x2* tab) {
+    return half_bits(f.d) * (run(f, 0, x, tab) + run(f, 1, x, tab));
+  }
+};
 
 struct GluParams {
   const uint8_t* gate;
   const uint8_t* up;
   const uint32_t* idx;  // expert of each pair
-  const u32x4* x;       // the token: 4096 float16 as 512 pieces of 16 bytes
+  const u32x4* x;       // the tokens: 4096 float16 each, as 512 pieces of 16 bytes
   f16* out_gate;        // gate . x (may be null)
   f16* out_up;          // up . x (may be null)
   f16* h;               // silu(gate . x) * (up . x)
   int64_t mat_bytes;
   uint32_t experts;
-  int rows, row_bytes, pairs, units, waves;
-  int wave_pairs, wave_rows;  // waves / rows and waves % rows: from a wave's unit to its next
+  int rows, row_bytes, pairs, share, tokens, waves;
+  // units: u = a * nb + b, (a, b) = (pair, row) for one token, (row, pair) for several; from a wave's unit to its
+  // next, (a, b) moves by (wave_a, wave_b) with a carry
+  int na, nb, wave_a, wave_b;
 };
 
-// Lane j's offsets within a row, without each field's constant offset in its block (that goes to the row's
-// address, which the whole wave shares): the loads then take a scalar base and a 32-bit lane offset.
-struct GluOffsets {
-  uint32_t d, qs, qh, sg, sc;
-};
-__device__ __forceinline__ GluOffsets glu_offsets(int j) {
-  const uint32_t b = (uint32_t)(j >> 2) * 110, jj = (uint32_t)j & 3;
-  return GluOffsets{b, b + 16 * jj, b + 2 * jj, b + 8 * jj, b + 2 * (jj >> 1)};
-}
+// The token's piece i (16 bytes) of lane j in LDS: slot 8 j + (i ^ j % 8), so that the eight lanes of one LDS
+// cycle of a 16-byte read fall on distinct banks.
+__device__ __forceinline__ int glu_x_slot(int j, int i) { return 8 * j + (i ^ (j & 7)); }
 
-// The fields of lane j's run pair in the row at `row` (IQ3_S: d @0, qs[64] @2, qh[8] @66, signs[32] @74,
-// scales[4] @106 of each 110-byte block).
-__device__ __forceinline__ void glu_load(const uint8_t* row, const GluOffsets& o, RunPair<K_IQ3_S>& f) {
-  f.d = load_at<uint16_t>(row, o.d);
-  f.qs = load_at<u32x4>(row + 2, o.qs);
-  f.qh = load_at<uint16_t>(row + 66, o.qh);
-  f.sg = load_at<u32x2>(row + 74, o.sg);
-  f.sc = load_at<uint16_t>(row + 106, o.sc);
-}
-
-// Run h (0, 1) of the pair: its 32 weights from the signed codebook, times 32 activations (16 packed pairs).
-// Group l's word: the index byte qs[l] low, the ninth bit and the sign nibble of group l high. The ninth bits
-// of the even groups (bits 0, 2, 4, 6 of the run's qh byte) go to bit 0 of bytes 0..3 by one multiply (the
-// products' other bits never reach bits 0, 8, 16, 24), the sign nibbles of the even groups are the low nibbles of
-// the run's four sign bytes; the odd groups take bits 1, 3, 5, 7 and the high nibbles.
-__device__ __forceinline__ float iq3s_run_signed(const RunPair<K_IQ3_S>& f, int h, const uint32_t* x,
-                                                 const u32x2* tab) {
-  const uint32_t q0 = f.qs[2 * h], q1 = f.qs[2 * h + 1];
-  const uint32_t hb = (uint32_t)f.qh >> (8 * h);
-  const uint32_t sg = f.sg[h];
-  const uint32_t he = (((hb & 0x55u) * 0x41041u) & 0x01010101u) | ((sg & 0x0F0F0F0Fu) << 1);
-  const uint32_t ho = ((((hb >> 1) & 0x55u) * 0x41041u) & 0x01010101u) | ((sg >> 3) & 0x1E1E1E1Eu);
-  const uint32_t w02 = __builtin_amdgcn_perm(he, q0, 0x05020400u), w13 = __builtin_amdgcn_perm(ho, q0, 0x05030401u);
-  const uint32_t w46 = __builtin_amdgcn_perm(he, q1, 0x07020600u), w57 = __builtin_amdgcn_perm(ho, q1, 0x07030601u);
-  const uint32_t three = 3;
-  const uint32_t a[8] = {word_shl<0>(w02, three), word_shl<0>(w13, three), word_shl<1>(w02, three),
-                         word_shl<1>(w13, three), word_shl<0>(w46, three), word_shl<0>(w57, three),
-                         word_shl<1>(w46, three), word_shl<1>(w57, three)};
-  uint32_t w[16];
-#pragma unroll
-  for (int l = 0; l < 8; ++l) {
-    const u32x2 v = lds_entry(tab, a[l]);
-    w[2 * l] = v[0];
-    w[2 * l + 1] = v[1];
-  }
-  return dot16x2(w, x + 16 * h);
-}
-
-// Lane j's share of a row: its two runs, each times its scale d (1 + 2 s).
-__device__ __forceinline__ float iq3s_pair_signed(const RunPair<K_IQ3_S>& f, int j, const uint32_t* x,
-                                                  const u32x2* tab) {
-  const float d = half_bits(f.d);
-  const uint32_t sc = (uint32_t)f.sc >> (8 * (j & 1));
-  const float s0 = d * (float)(1 + 2 * (sc & 15u)), s1 = d * (float)(1 + 2 * ((sc >> 4) & 15u));
-  return s0 * iq3s_run_signed(f, 0, x, tab) + s1 * iq3s_run_signed(f, 1, x, tab);
-}
-
-// The unit's two rows decoded and multiplied, and their sums met over the wave: the gate row's total and the up
-// row's, the same in every lane (read once into scalars).
+// The unit's gate and up rows decoded and multiplied, and their sums met over the wave: the gate row's total and
+// the up row's, the same in every lane (read into scalars).
 template <int KIND>
-__device__ __forceinline__ void glu_unit(RunPair<KIND> (&f)[2], int lane, const uint32_t* x, const u32x2* tab,
-                                         float& gate, float& up) {
+__device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], int lane, const uint32_t* x,
+                                         const u32x2* tab, float& gate, float& up) {
   opaque(f[0]);  // nothing of the decode is done before the workgroup barrier (it would wait for these rows there)
   opaque(f[1]);
-  float g = iq3s_pair_signed(f[0], lane, x, tab);
-  float u = iq3s_pair_signed(f[1], lane, x, tab);
+  float g = Routed<KIND>::pair_sum(f[0], lane, x, tab);
+  float u = Routed<KIND>::pair_sum(f[1], lane, x, tab);
   // lanes 0-31 the gate row's partial sums two at a time, lanes 32-63 the up row's; then within the halves
   float v = sum_swapped(g, u, 32);
   v = sum_swapped(v, v, 16);
@@ -128,37 +191,41 @@ __device__ __forceinline__ void glu_unit(RunPair<KIND> (&f)[2], int lane, const 
   up = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
-// The token in LDS: piece c (16 bytes) of lane j = c / 8 at slot 8 j + (c % 8 ^ j % 8), so that the eight lanes
-// of one LDS cycle of a 16-byte read fall on distinct banks.
-__device__ __forceinline__ int glu_x_slot(int j, int i) { return 8 * j + (i ^ (j & 7)); }
-
-template <int KIND, int UPW>
+// MULTI: several tokens, in LDS, each unit reading its own; else one token, held in registers.
+template <int KIND, int UPW, bool MULTI>
 __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p) {
-  static_assert(KIND == K_IQ3_S, "the signed codebook is IQ3_S's");
+  typedef Routed<KIND> R;
+  typedef typename R::Fields Fields;
   constexpr int kBuffers = UPW < 3 ? UPW : 3;  // units whose rows are in registers at once
-  __shared__ u32x2 tab[kGluEntries];
-  __shared__ u32x4 xs[512];
+  constexpr int kTokens = MULTI ? kGluMaxTokens : 1;
+  __shared__ u32x2 tab[R::kEntries];
+  __shared__ u32x4 xs[512 * kTokens];
   const int tid = threadIdx.x, lane = tid & 63;
   const int gw = blockIdx.x * kGluWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // what the workgroup shares, asked for first: the codebook entry this thread expands and a piece of the token
-  const uint64_t entry = kIq3sHalfGrid.v[tid & 511];
-  const u32x4 xpiece = p.x[tid & 511];
-  // the wave's units and their experts
+  // what the workgroup shares, asked for first: the table entry this thread expands and pieces of the tokens
+  const uint64_t entry = R::fetch(tid);
+  constexpr int kPieceLoads = (512 * kTokens + kGluThreads - 1) / kGluThreads;
+  u32x4 xpiece[kPieceLoads];
+#pragma unroll
+  for (int k = 0; k < kPieceLoads; ++k) xpiece[k] = p.x[min(tid + k * kGluThreads, 512 * p.tokens - 1)];
+
+  // the wave's units: (pair, row), live, and the o of its outputs
   int pair[UPW], row[UPW];
   bool live[UPW];
   {
-    int pr = gw / p.rows, r = gw - pr * p.rows;
+    int a = gw / p.nb, b = gw - a * p.nb;
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
-      live[k] = pr < p.pairs;
-      pair[k] = live[k] ? pr : p.pairs - 1;  // past the last unit: the last unit's rows again, nothing written
+      live[k] = a < p.na;
+      const int pr = MULTI ? b : a, r = MULTI ? a : b;
+      pair[k] = live[k] ? pr : p.pairs - 1;  // past the last unit: the last pair's last row again, nothing written
       row[k] = live[k] ? r : p.rows - 1;
-      r += p.wave_rows;
-      pr += p.wave_pairs;
-      if (r >= p.rows) {
-        r -= p.rows;
-        ++pr;
+      b += p.wave_b;
+      a += p.wave_a;
+      if (b >= p.nb) {
+        b -= p.nb;
+        ++a;
       }
     }
   }
@@ -170,61 +237,52 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
     bad[k] = e >= p.experts;
     expert[k] = bad[k] ? 0u : e;  // a pair naming no expert reads expert 0's rows and writes NaN
   }
-  const GluOffsets lo = glu_offsets(lane);
-  auto issue = [&](int k, RunPair<KIND>(&f)[2]) {
+  auto issue = [&](int k, Fields(&f)[2]) {
     const int64_t off = (int64_t)expert[k] * p.mat_bytes + (int64_t)row[k] * p.row_bytes;
-    glu_load(p.gate + off, lo, f[0]);
-    glu_load(p.up + off, lo, f[1]);
+    R::load(p.gate + off, lane, f[0]);
+    R::load(p.up + off, lane, f[1]);
     asm volatile("" ::: "memory");  // the units' loads go out in unit order
   };
 
-  // the signed codebook: this thread's grid entry under eight of the 16 sign nibbles; the token's pieces
-  {
-    const uint32_t lo32 = (uint32_t)entry, hi32 = (uint32_t)(entry >> 32);
-    const int half = tid >> 9;
+  R::fill(tab, tid, entry);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int s = 8 * half + i;
-      const uint32_t m0 = ((i & 1) ? 0x8000u : 0u) | ((i & 2) ? 0x80000000u : 0u);
-      const uint32_t m1 = ((i & 4) ? 0x8000u : 0u) | (half ? 0x80000000u : 0u);
-      tab[s * 512 + (tid & 511)] = u32x2{lo32 ^ m0, hi32 ^ m1};
-    }
-    xs[glu_x_slot((tid & 511) >> 3, tid & 7)] = xpiece;  // two threads a piece: the same bytes
+  for (int k = 0; k < kPieceLoads; ++k) {
+    const int c = min(tid + k * kGluThreads, 512 * p.tokens - 1);  // threads past the pieces write one again
+    xs[(c >> 9) * 512 + glu_x_slot((c & 511) >> 3, c & 7)] = xpiece[k];
   }
   __syncthreads();
   uint32_t x[32];
+  auto read_x = [&](int t) {
 #pragma unroll
-  for (int v = 0; v < 8; ++v) {
-    const u32x4 c = xs[glu_x_slot(lane, v)];
+    for (int v = 0; v < 8; ++v) {
+      const u32x4 c = xs[t * 512 + glu_x_slot(lane, v)];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
-  }
-  RunPair<KIND> f[kBuffers][2];
+      for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
+    }
+  };
+  if constexpr (!MULTI) read_x(0);
+  Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
 
-  float gate[UPW], up[UPW];
+  // lane k collects unit k's gate and up totals
+  float gv = 0.0f, uv = 0.0f;
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    glu_unit<KIND>(f[k % kBuffers], lane, x, tab, gate[k], up[k]);
+    if constexpr (MULTI) read_x(pair[k] / p.share);
+    float g, u;
+    glu_unit<KIND>(f[k % kBuffers], lane, x, tab, g, u);
     if (k + kBuffers < UPW) issue(k + kBuffers, f[k % kBuffers]);
+    gv = lane == k ? g : gv;
+    uv = lane == k ? u : uv;
   }
 
   // lane k writes unit k: gate, up and silu(gate) * up as mlx-lm rounds it
-  float gv = gate[0], uv = up[0];
-#pragma unroll
-  for (int k = 1; k < UPW; ++k) {
-    gv = lane == k ? gate[k] : gv;
-    uv = lane == k ? up[k] : uv;
-  }
-  int my = 0;
-#pragma unroll
-  for (int k = 1; k < UPW; ++k) my = lane == k ? k : my;
   bool w_live = false, w_bad = false;
   int w_pair = 0, w_row = 0;
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    if (my == k) {
+    if (lane == k) {
       w_live = live[k];
       w_bad = bad[k];
       w_pair = pair[k];
@@ -245,10 +303,10 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   }
 }
 
-// Down (and any one-matrix routed product) on IQ3_S rows of 1536 or 2560 inputs: 8 lanes take a row, lane m its
-// run pairs m, m + 8, ... (S of them), so a wave holds 8 rows (a unit). A workgroup (one a CU) takes consecutive
-// units of one pair, whose token sits in LDS beside the signed codebook; the rows go out after the barrier, as
-// in routed_glu_kernel, and a row's sum meets over its 8 lanes by three DPP steps.
+// Down (and any one-matrix routed product) on rows of 1536 or 2560 inputs: 8 lanes take a row, lane m its run
+// pairs m, m + 8, ... (S of them), so a wave holds 8 rows (a unit). A workgroup (one a CU) takes consecutive units
+// of one pair, whose token sits in LDS beside the table; the rows go out after the barrier, as in
+// routed_glu_kernel, and a row's sum meets over its 8 lanes by three DPP steps.
 struct DownParams {
   const uint8_t* blocks;
   const uint32_t* idx;
@@ -260,18 +318,19 @@ struct DownParams {
   int groups_per_pair;  // workgroups a pair
 };
 
-template <int S, int UPW>
+template <int KIND, int S, int UPW>
 __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams p) {
+  typedef Routed<KIND> R;
   constexpr int kPairs = 8 * S;        // run pairs of a row
   constexpr int kPieces = 8 * kPairs;  // 16-byte pieces of a token
-  __shared__ u32x2 tab[kGluEntries];
+  __shared__ u32x2 tab[R::kEntries];
   __shared__ u32x4 xs[kPieces];
   const int tid = threadIdx.x, lane = tid & 63, m = lane & 7, sub = lane >> 3;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int pair = blockIdx.x / p.groups_per_pair, chunk = blockIdx.x - pair * p.groups_per_pair;
 
-  // the codebook entry this thread expands and a piece of the pair's token, asked for first
-  const uint64_t entry = kIq3sHalfGrid.v[tid & 511];
+  // the table entry this thread expands and a piece of the pair's token, asked for first
+  const uint64_t entry = R::fetch(tid);
   const u32x4 xpiece = reinterpret_cast<const u32x4*>(p.x + (int64_t)(pair / p.share) * (8 * kPieces))[tid % kPieces];
   const uint32_t e = p.idx[pair];
   const bool bad = e >= p.experts;
@@ -279,28 +338,20 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams 
   int r0[UPW];
 #pragma unroll
   for (int k = 0; k < UPW; ++k) r0[k] = ((chunk * kGluWaves + wave) * UPW + k) * 8;  // the unit's first row
+  R::fill(tab, tid, entry);
   {
-    const uint32_t lo32 = (uint32_t)entry, hi32 = (uint32_t)(entry >> 32);
-    const int half = tid >> 9;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int s = 8 * half + i;
-      const uint32_t m0 = ((i & 1) ? 0x8000u : 0u) | ((i & 2) ? 0x80000000u : 0u);
-      const uint32_t m1 = ((i & 4) ? 0x8000u : 0u) | (half ? 0x80000000u : 0u);
-      tab[s * 512 + (tid & 511)] = u32x2{lo32 ^ m0, hi32 ^ m1};
-    }
     const int c = tid % kPieces;  // threads past the token's pieces write the same bytes again
     xs[glu_x_slot(c >> 3, c & 7)] = xpiece;
   }
   __syncthreads();
 
-  RunPair<K_IQ3_S> f[UPW][S];
+  typename R::Fields f[UPW][S];
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
     const int rl = min(r0[k] + sub, p.rows - 1);  // rows past the matrix read its last row, and write nothing
     const uint8_t* row = mat + (int64_t)rl * p.row_bytes;
 #pragma unroll
-    for (int st = 0; st < S; ++st) glu_load(row, glu_offsets(8 * st + m), f[k][st]);
+    for (int st = 0; st < S; ++st) R::load(row, 8 * st + m, f[k][st]);
     asm volatile("" ::: "memory");
   }
 #pragma unroll
@@ -317,7 +368,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams 
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
       }
-      acc += iq3s_pair_signed(f[k][st], j, x, tab);
+      acc += R::pair_sum(f[k][st], j, x, tab);
     }
     acc += lanes_apart(acc, 1);
     acc += lanes_apart(acc, 2);
@@ -327,28 +378,30 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams 
   }
 }
 
-// Whether routed_down_kernel takes a routed one-matrix call: IQ3_S rows of 1536 or 2560 inputs, float16 in and
-// out (the caller has checked the dtypes).
+constexpr bool routed_kind(int kind) { return kind == K_IQ3_S || kind == K_Q2_0; }
+
+// Whether routed_down_kernel takes a routed one-matrix call: IQ3_S or Q2_0 rows of 1536 or 2560 inputs, float16
+// in and out (the caller has checked the dtypes).
 template <int KIND>
 bool routed_down_takes(const MatvecParams& p) {
-  return KIND == K_IQ3_S && p.mode == MODE_EXPERT && (p.cols == 1536 || p.cols == 2560) &&
+  return routed_kind(KIND) && p.mode == MODE_EXPERT && (p.cols == 1536 || p.cols == 2560) &&
          p.glu_out == nullptr && p.experts <= INT32_MAX && p.pairs <= 65535;
 }
 
-template <int S, int UPW>
+template <int KIND, int S, int UPW>
 int launch_down_su(DownParams& p, int units_per_pair, hipStream_t s) {
   const int per_group = kGluWaves * UPW;
   p.groups_per_pair = (units_per_pair + per_group - 1) / per_group;
   const int64_t groups = (int64_t)p.groups_per_pair * p.pairs;
   if (groups > INT32_MAX) return STRATA_ERR_SHAPE;
-  hipLaunchKernelGGL((routed_down_kernel<S, UPW>), dim3((unsigned)groups), dim3(kGluThreads), 0, s, p);
+  hipLaunchKernelGGL((routed_down_kernel<KIND, S, UPW>), dim3((unsigned)groups), dim3(kGluThreads), 0, s, p);
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }
 
 template <int KIND>
 int launch_routed_down(const MatvecParams& mp, hipStream_t s) {
-  if constexpr (KIND != K_IQ3_S) {
+  if constexpr (!routed_kind(KIND)) {
     return STRATA_ERR_SHAPE;
   } else {
     DownParams p = {};
@@ -366,22 +419,38 @@ int launch_routed_down(const MatvecParams& mp, hipStream_t s) {
     const int64_t units = (int64_t)units_per_pair * mp.pairs;
     const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * kGluWaves;
     const bool two = units > capacity;  // more units than one round of waves: two a wave
-    if (mp.cols == 1536) return two ? launch_down_su<3, 2>(p, units_per_pair, s) : launch_down_su<3, 1>(p, units_per_pair, s);
-    return two ? launch_down_su<5, 2>(p, units_per_pair, s) : launch_down_su<5, 1>(p, units_per_pair, s);
+    if (mp.cols == 1536)
+      return two ? launch_down_su<KIND, 3, 2>(p, units_per_pair, s) : launch_down_su<KIND, 3, 1>(p, units_per_pair, s);
+    return two ? launch_down_su<KIND, 5, 2>(p, units_per_pair, s) : launch_down_su<KIND, 5, 1>(p, units_per_pair, s);
   }
 }
 
-// Whether routed_glu_kernel takes a paired gate/up call: IQ3_S rows of 4096 inputs, one token for every pair,
-// float16 in and out (the caller has checked the dtypes).
+// Whether routed_glu_kernel takes a paired gate/up call: IQ3_S or Q2_0 rows of 4096 inputs, at most eight
+// tokens, float16 in and out (the caller has checked the dtypes).
 template <int KIND>
 bool routed_glu_takes(const MatvecParams& p) {
-  return KIND == K_IQ3_S && p.mode == MODE_EXPERT && p.cols == 4096 && p.share == p.pairs && p.glu_out != nullptr &&
-         p.experts <= INT32_MAX && (int64_t)p.pairs * p.rows <= INT32_MAX / 2;
+  return routed_kind(KIND) && p.mode == MODE_EXPERT && p.cols == 4096 && p.glu_out != nullptr &&
+         p.pairs / p.share <= kGluMaxTokens && p.experts <= INT32_MAX && (int64_t)p.pairs * p.rows <= INT32_MAX / 2;
+}
+
+template <int KIND, bool MULTI>
+int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
+  const dim3 block(kGluThreads);
+  switch (upw) {
+    case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MULTI>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((routed_glu_kernel<KIND, 3, MULTI>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((routed_glu_kernel<KIND, 4, MULTI>), grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL((routed_glu_kernel<KIND, 6, MULTI>), grid, block, 0, s, p); break;
+    case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MULTI>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MULTI>), grid, block, 0, s, p); break;
+  }
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
 }
 
 template <int KIND>
 int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
-  if constexpr (KIND != K_IQ3_S) {
+  if constexpr (!routed_kind(KIND)) {
     return STRATA_ERR_SHAPE;
   } else {
     GluParams p = {};
@@ -397,24 +466,29 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
     p.rows = mp.rows;
     p.row_bytes = mp.row_bytes;
     p.pairs = mp.pairs;
-    p.units = mp.pairs * mp.rows;
+    p.share = mp.share;
+    p.tokens = mp.pairs / mp.share;
+    const bool multi = p.tokens > 1;
+    p.na = multi ? p.rows : p.pairs;
+    p.nb = multi ? p.pairs : p.rows;
+    const int units = p.pairs * p.rows;
     const int capacity = device_cus() * kGluGroupsPerCU * kGluWaves;
-    int upw = (p.units + capacity - 1) / capacity;
-    upw = upw < 1 ? 1 : (upw > kGluMaxUnits ? kGluMaxUnits : upw);
-    const int64_t waves = ((int64_t)(p.units + upw - 1) / upw + kGluWaves - 1) / kGluWaves * kGluWaves;
+    int need = (units + capacity - 1) / capacity;
+    // the forms built (two and eight units a wave spill a few registers in IQ3_S)
+    static const int kForms[] = {1, 3, 4, 6, 12, 16};
+    int upw = kGluMaxUnits;
+    for (int f : kForms)
+      if (f >= need) {
+        upw = f;
+        break;
+      }
+    const int64_t waves = ((int64_t)(units + upw - 1) / upw + kGluWaves - 1) / kGluWaves * kGluWaves;
     if (waves / kGluWaves > INT32_MAX) return STRATA_ERR_SHAPE;
     p.waves = (int)waves;
-    p.wave_pairs = p.waves / p.rows;
-    p.wave_rows = p.waves % p.rows;
+    p.wave_a = p.waves / p.nb;
+    p.wave_b = p.waves % p.nb;
     const dim3 grid((unsigned)(waves / kGluWaves));
-    switch (upw) {
-      case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1>), grid, dim3(kGluThreads), 0, s, p); break;
-      case 2: hipLaunchKernelGGL((routed_glu_kernel<KIND, 2>), grid, dim3(kGluThreads), 0, s, p); break;
-      case 3: hipLaunchKernelGGL((routed_glu_kernel<KIND, 3>), grid, dim3(kGluThreads), 0, s, p); break;
-      default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 4>), grid, dim3(kGluThreads), 0, s, p); break;
-    }
-    STRATA_CHECK_LAUNCH();
-    return STRATA_OK;
+    return multi ? launch_glu_upw<KIND, true>(p, upw, grid, s) : launch_glu_upw<KIND, false>(p, upw, grid, s);
   }
 }
 
