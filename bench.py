@@ -13,9 +13,10 @@ Beside it, on the same line, the other workloads of the path:
   q4k_matvec     one Q4_K 4096 x 4096 matrix, float32 x, batch 1 (graphs of 64 distinct copies), and its CPU path
   prompt         512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, the fused
                  gate/up/SwiGLU and scatter-down MFMA kernels; TFLOPS over the real pairs' 2 * pairs * 3 * H * F
-  dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K, o Q8_0, the shared
-                 expert's Q4_K gate / up 1536 x 4096 and down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16
-                 token each (graphs over copies, at least 1 GB a graph)
+  dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K fused into one launch, o
+                 Q8_0, the shared expert's Q4_K gate and up 1536 x 4096 with the SwiGLU in one launch and its
+                 down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16 token each (graphs over copies, at least
+                 1 GB a graph)
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
                  the dense layers as tile products, TFLOPS
   roofline       the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
@@ -161,28 +162,41 @@ def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512):
             "hbm_bound_tflops": round(2.0 * tokens * K * 3 * H * F / (3 * E * F * H / 256 * 98) * HBM_PEAK_GBS / 1e3, 1)}
 
 
-DENSE = [("q", "Q6_K", 4096, 4096), ("k", "Q6_K", 4096, 4096), ("v", "Q6_K", 4096, 4096), ("o", "Q8_0", 4096, 4096),
-         ("shared_gate", "Q4_K", 1536, 4096), ("shared_up", "Q4_K", 1536, 4096), ("shared_down", "Q4_K", 4096, 1536),
-         ("lm_head", "Q6_K", 151936, 4096)]
+# The dense layers of a mixed-model decode token, as an engine runs them: q, k and v fused into one 12288-row
+# layer (dense.FusedLinear), the shared expert's gate and up with the SwiGLU in one launch (dense.gate_up_swiglu).
+DENSE = [("qkv", "Q6_K", 3 * 4096, 4096, "matvec"), ("o", "Q8_0", 4096, 4096, "matvec"),
+         ("shared_gate_up", "Q4_K", 2 * 1536, 4096, "glu"), ("shared_down", "Q4_K", 4096, 1536, "matvec"),
+         ("lm_head", "Q6_K", 151936, 4096, "matvec")]
 
 
 def dense_bench(B, synth, dev, steps, warmup):
-    """Each dense matvec of a decode token at one token: mean time over a graph of distinct copies."""
+    """Each dense launch of a decode token at one token: mean time over a graph of distinct copies."""
+    from strata_mlx_amd import dense as D
     g = torch.Generator(device=dev)
     g.manual_seed(2)
     out, total_bytes, total_s = {}, 0, 0.0
-    for name, kind, rows, cols in DENSE:
+    for name, kind, rows, cols, how in DENSE:
         per, bb = synth.DENSE.get(kind) or synth.BLOCK[kind]
         nbytes = rows * cols // per * bb
         copies = max(2, -(-(1 << 30) // nbytes))
         mats = [synth.random_stack(kind, rows * cols, dev, g) for _ in range(copies)]
         x = (torch.randn((1, cols), device=dev) / 8).half()
+        if how == "glu":  # gate: the first half of the rows, up: the second
+            half = rows // 2 * (cols // per * bb)
+            layers = [(D.BlockLinear(m[:half], kind, (rows // 2, cols)), D.BlockLinear(m[half:], kind, (rows // 2, cols)))
+                      for m in mats]
+
+            def run(i):
+                D.gate_up_swiglu(layers[i][0], layers[i][1], x)
+        else:
+            def run(i):
+                B.window_matvec(mats[i], kind, rows, cols, x)
         graph = torch.cuda.CUDAGraph()
-        B.window_matvec(mats[0], kind, rows, cols, x)
+        run(0)
         torch.cuda.synchronize()
         with torch.cuda.graph(graph):
-            for m in mats:
-                B.window_matvec(m, kind, rows, cols, x)
+            for i in range(copies):
+                run(i)
         t = time_graph(graph, steps, warmup) / steps / copies
         out[name] = {"kind": kind, "rows": rows, "cols": cols, "us": round(t * 1e6, 2),
                      "gbs": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
@@ -292,13 +306,14 @@ def q4k_bench(B, synth, dev, steps, warmup, copies=64):
 
 def prefill_bench(B, D, synth, dev, lins, steps, warmup, rng, tokens=2048):
     """A 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts of `lins` (Zipf top-8) through
-    the tiles, and the dense layers (q, k, v Q6_K, o Q8_0, the shared expert's Q4_K gate, up, down) as tile products
-    of the whole chunk. Returns TFLOPS over the real products' flops, each part and all."""
+    the tiles, and the dense layers (q, k, v Q6_K fused, o Q8_0, the shared expert's Q4_K gate and up fused, down) as
+    tile products of the whole chunk. Returns TFLOPS over the real products' flops, each part and all."""
     g = torch.Generator(device=dev)
     g.manual_seed(4)
-    dense = [D.BlockLinear(synth.random_stack(kind, r * c, dev, g), kind, (r, c))
-             for kind, r, c in (("Q6_K", H, H), ("Q6_K", H, H), ("Q6_K", H, H), ("Q8_0", H, H), ("Q4_K", F, H),
-                                ("Q4_K", F, H), ("Q4_K", H, F))]
+    mk = lambda kind, r, c: D.BlockLinear(synth.random_stack(kind, r * c, dev, g), kind, (r, c))
+    # q, k, v as one layer and the shared expert's gate and up as one, as the decode runs them
+    dense = [D.FusedLinear([mk("Q6_K", H, H) for _ in range(3)]), mk("Q8_0", H, H),
+             D.FusedLinear([mk("Q4_K", F, H) for _ in range(2)]), mk("Q4_K", H, F)]
     idx = [torch.from_numpy(synth.zipf_routing(tokens, E, K, rng)[0]).to(torch.int32).to(dev) for _ in lins]
     x = torch.randn((tokens, H), device=dev).to(torch.bfloat16)
     xf = torch.randn((tokens, F), device=dev).to(torch.bfloat16)

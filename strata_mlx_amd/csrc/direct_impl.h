@@ -1315,7 +1315,9 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
       const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
                                                                      : (glu ? p.pairs <= 16
                                                                             : p.pairs <= p.share || p.pairs <= 8));
+      if (!glu && routed_one_takes<KIND>(p)) return launch_routed_one<KIND>(p, s);
       if (p.glu_out != nullptr) {
+        if (!glu && grid_z == 2 && routed_glu_takes<KIND>(p)) return launch_routed_glu<KIND>(p, s);
         if (glu || grid_z != 2) return STRATA_ERR_SHAPE;
         return launch_direct<KIND, false, true>(p, one, grid_y, grid_z, s);
       }

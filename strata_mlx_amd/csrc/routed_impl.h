@@ -44,13 +44,35 @@ constexpr int kGluMaxUnits = 16;   // units a wave (straight-line code); more un
 constexpr int kGluMaxTokens = 8;   // tokens in LDS
 
 // What a type brings to these kernels: its LDS table (built by the workgroup), the fields of a lane's run pair
-// (64 weights), their loads and the lane's share of a row's sum.
+// (64 weights), their loads, the lane's share of a row's sum, and how many units' fields fit in registers at
+// once. This form is the linear types' (Q4_K, Q6_K, Q8_0): the direct kernel's register decode, no table.
 template <int KIND>
-struct Routed;
+struct Routed {
+  static constexpr int kEntries = 1;
+  static constexpr int kBuffers = KIND == K_Q6_K ? 1 : 2;  // Q6_K's 18 registers a run pair spill at two
+  typedef RunPair<KIND> Fields;
+  static __device__ __forceinline__ uint64_t fetch(int) { return 0; }
+  static __device__ __forceinline__ void fill(u32x2*, int, uint64_t) {}
+  static __device__ __forceinline__ void load(const uint8_t* row, int j, Fields& f) {
+    load_fields<KIND>(row, 0u, lane_offsets<KIND>(j), f);
+  }
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const u32x2* tab) {
+    const DirectTables<KIND>& t = *reinterpret_cast<const DirectTables<KIND>*>(tab);  // unused by these types
+    float s = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w[16];
+      const RunScale rs = decode_run<KIND>(f, h, j, w, t);
+      s += apply_run<KIND>(rs, w, x + 16 * h);
+    }
+    return s;
+  }
+};
 
 template <>
 struct Routed<K_IQ3_S> {
   static constexpr int kEntries = 8192;  // 512 grid entries x 16 sign nibbles
+  static constexpr int kBuffers = 3;
   typedef RunPair<K_IQ3_S> Fields;
   // the codebook entry thread tid expands (asked for before anything else)
   static __device__ __forceinline__ uint64_t fetch(int tid) { return kIq3sHalfGrid.v[tid & 511]; }
@@ -115,6 +137,7 @@ struct Routed<K_IQ3_S> {
 template <>
 struct Routed<K_Q2_0> {
   static constexpr int kEntries = 256;  // a code byte's four weights c - 1 as float16
+  static constexpr int kBuffers = 3;
   typedef RunPair<K_Q2_0> Fields;
   static __device__ __forceinline__ uint64_t fetch(int) { return 0; }
   static __device__ __forceinline__ void fill(u32x2* tab, int tid, uint64_t) {
@@ -151,12 +174,16 @@ struct Routed<K_Q2_0> {
   }
 };
 
+// GLU1: gate and up of one token (a unit: row r of each); GLUN: the same at several tokens, in LDS; ONE: one
+// matrix and one token, no routing (a unit: rows 2 i and 2 i + 1).
+enum GluMode : int { GLU1 = 0, GLUN = 1, ONE = 2 };
+
 struct GluParams {
-  const uint8_t* gate;
+  const uint8_t* gate;  // ONE: the matrix
   const uint8_t* up;
-  const uint32_t* idx;  // expert of each pair
+  const uint32_t* idx;  // expert of each pair (ONE: none)
   const u32x4* x;       // the tokens: 4096 float16 each, as 512 pieces of 16 bytes
-  f16* out_gate;        // gate . x (may be null)
+  f16* out_gate;        // gate . x (may be null); ONE: the product
   f16* out_up;          // up . x (may be null)
   f16* h;               // silu(gate . x) * (up . x)
   int64_t mat_bytes;
@@ -167,12 +194,14 @@ struct GluParams {
   int na, nb, wave_a, wave_b;
 };
 
-// The token's piece i (16 bytes) of lane j in LDS: slot 8 j + (i ^ j % 8), so that the eight lanes of one LDS
-// cycle of a 16-byte read fall on distinct banks.
+// A token's piece c (16 bytes: columns 8 c .. 8 c + 7) in LDS: slot c with its low three bits XORed with the
+// next three, so that the eight lanes of one LDS cycle of a 16-byte read (pieces 8 j + i of lanes j) fall on
+// distinct banks.
 __device__ __forceinline__ int glu_x_slot(int j, int i) { return 8 * j + (i ^ (j & 7)); }
+__device__ __forceinline__ int x_piece_slot(int c) { return glu_x_slot(c >> 3, c & 7); }
 
-// The unit's gate and up rows decoded and multiplied, and their sums met over the wave: the gate row's total and
-// the up row's, the same in every lane (read into scalars).
+// The unit's two rows decoded and multiplied (gate and up, or rows 2 i and 2 i + 1), and their sums met over the
+// wave: the first row's total and the second's, the same in every lane (read into scalars).
 template <int KIND>
 __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], int lane, const uint32_t* x,
                                          const u32x2* tab, float& gate, float& up) {
@@ -180,7 +209,7 @@ __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], 
   opaque(f[1]);
   float g = Routed<KIND>::pair_sum(f[0], lane, x, tab);
   float u = Routed<KIND>::pair_sum(f[1], lane, x, tab);
-  // lanes 0-31 the gate row's partial sums two at a time, lanes 32-63 the up row's; then within the halves
+  // lanes 0-31 the first row's partial sums two at a time, lanes 32-63 the second's; then within the halves
   float v = sum_swapped(g, u, 32);
   v = sum_swapped(v, v, 16);
   v += lanes_apart(v, 8);
@@ -191,13 +220,12 @@ __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], 
   up = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
-// MULTI: several tokens, in LDS, each unit reading its own; else one token, held in registers.
-template <int KIND, int UPW, bool MULTI>
+template <int KIND, int UPW, int MODE>
 __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p) {
   typedef Routed<KIND> R;
   typedef typename R::Fields Fields;
-  constexpr int kBuffers = UPW < 3 ? UPW : 3;  // units whose rows are in registers at once
-  constexpr int kTokens = MULTI ? kGluMaxTokens : 1;
+  constexpr int kBuffers = UPW < R::kBuffers ? UPW : R::kBuffers;  // units whose rows are in registers at once
+  constexpr int kTokens = MODE == GLUN ? kGluMaxTokens : 1;
   __shared__ u32x2 tab[R::kEntries];
   __shared__ u32x4 xs[512 * kTokens];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -210,7 +238,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
 #pragma unroll
   for (int k = 0; k < kPieceLoads; ++k) xpiece[k] = p.x[min(tid + k * kGluThreads, 512 * p.tokens - 1)];
 
-  // the wave's units: (pair, row), live, and the o of its outputs
+  // the wave's units (pair, row) and whether each is live; ONE: row is the unit's first row (2 i), pair 0
   int pair[UPW], row[UPW];
   bool live[UPW];
   {
@@ -218,9 +246,14 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
       live[k] = a < p.na;
-      const int pr = MULTI ? b : a, r = MULTI ? a : b;
-      pair[k] = live[k] ? pr : p.pairs - 1;  // past the last unit: the last pair's last row again, nothing written
-      row[k] = live[k] ? r : p.rows - 1;
+      const int pr = MODE == GLUN ? b : a, r = MODE == GLUN ? a : b;
+      if constexpr (MODE == ONE) {
+        pair[k] = 0;
+        row[k] = live[k] ? 2 * b : 0;  // past the last unit: the first rows again, nothing written
+      } else {
+        pair[k] = live[k] ? pr : p.pairs - 1;  // past the last unit: the last pair's last row again, nothing written
+        row[k] = live[k] ? r : p.rows - 1;
+      }
       b += p.wave_b;
       a += p.wave_a;
       if (b >= p.nb) {
@@ -233,14 +266,25 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   bool bad[UPW];
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    const uint32_t e = p.idx[pair[k]];
-    bad[k] = e >= p.experts;
-    expert[k] = bad[k] ? 0u : e;  // a pair naming no expert reads expert 0's rows and writes NaN
+    if constexpr (MODE == ONE) {
+      bad[k] = false;
+      expert[k] = 0u;
+    } else {
+      const uint32_t e = p.idx[pair[k]];
+      bad[k] = e >= p.experts;
+      expert[k] = bad[k] ? 0u : e;  // a pair naming no expert reads expert 0's rows and writes NaN
+    }
   }
   auto issue = [&](int k, Fields(&f)[2]) {
-    const int64_t off = (int64_t)expert[k] * p.mat_bytes + (int64_t)row[k] * p.row_bytes;
-    R::load(p.gate + off, lane, f[0]);
-    R::load(p.up + off, lane, f[1]);
+    if constexpr (MODE == ONE) {
+      const uint8_t* r0 = p.gate + (int64_t)row[k] * p.row_bytes;
+      R::load(r0, lane, f[0]);
+      R::load(row[k] + 1 < p.rows ? r0 + p.row_bytes : r0, lane, f[1]);  // an odd last row: the same row twice
+    } else {
+      const int64_t off = (int64_t)expert[k] * p.mat_bytes + (int64_t)row[k] * p.row_bytes;
+      R::load(p.gate + off, lane, f[0]);
+      R::load(p.up + off, lane, f[1]);
+    }
     asm volatile("" ::: "memory");  // the units' loads go out in unit order
   };
 
@@ -248,28 +292,33 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
 #pragma unroll
   for (int k = 0; k < kPieceLoads; ++k) {
     const int c = min(tid + k * kGluThreads, 512 * p.tokens - 1);  // threads past the pieces write one again
-    xs[(c >> 9) * 512 + glu_x_slot((c & 511) >> 3, c & 7)] = xpiece[k];
+    xs[(c >> 9) * 512 + x_piece_slot(c & 511)] = xpiece[k];
   }
   __syncthreads();
+  // lane j's activations: the 32 columns of each of its two runs
   uint32_t x[32];
   auto read_x = [&](int t) {
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const u32x4 c = xs[t * 512 + glu_x_slot(lane, v)];
+    for (int h = 0; h < 2; ++h) {
+      const int r = run_of<KIND>(lane, h);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
+      for (int v = 0; v < 4; ++v) {
+        const u32x4 c = xs[t * 512 + x_piece_slot(4 * r + v)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[16 * h + 4 * v + i] = c[i];
+      }
     }
   };
-  if constexpr (!MULTI) read_x(0);
+  if constexpr (MODE != GLUN) read_x(0);
   Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
 
-  // lane k collects unit k's gate and up totals
+  // lane k collects unit k's two totals
   float gv = 0.0f, uv = 0.0f;
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    if constexpr (MULTI) read_x(pair[k] / p.share);
+    if constexpr (MODE == GLUN) read_x(pair[k] / p.share);
     float g, u;
     glu_unit<KIND>(f[k % kBuffers], lane, x, tab, g, u);
     if (k + kBuffers < UPW) issue(k + kBuffers, f[k % kBuffers]);
@@ -277,7 +326,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
     uv = lane == k ? u : uv;
   }
 
-  // lane k writes unit k: gate, up and silu(gate) * up as mlx-lm rounds it
+  // lane k writes unit k: gate, up and silu(gate) * up as mlx-lm rounds it; ONE: the two rows' products
   bool w_live = false, w_bad = false;
   int w_pair = 0, w_row = 0;
 #pragma unroll
@@ -290,16 +339,21 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
     }
   }
   if (lane < UPW && w_live) {
-    const int64_t o = (int64_t)w_pair * p.rows + w_row;
-    f16 gq = from_f32<f16>(gv), uq = from_f32<f16>(uv), hq;
-    if (w_bad) {
-      gq = uq = hq = (f16)__builtin_nanf("");
+    if constexpr (MODE == ONE) {
+      p.out_gate[w_row] = from_f32<f16>(gv);
+      if (w_row + 1 < p.rows) p.out_gate[w_row + 1] = from_f32<f16>(uv);
     } else {
-      hq = from_f32<f16>(swiglu_rounded<f16>(gq, uq));
+      const int64_t o = (int64_t)w_pair * p.rows + w_row;
+      f16 gq = from_f32<f16>(gv), uq = from_f32<f16>(uv), hq;
+      if (w_bad) {
+        gq = uq = hq = (f16)__builtin_nanf("");
+      } else {
+        hq = from_f32<f16>(swiglu_rounded<f16>(gq, uq));
+      }
+      if (p.out_gate != nullptr) p.out_gate[o] = gq;
+      if (p.out_up != nullptr) p.out_up[o] = uq;
+      p.h[o] = hq;
     }
-    if (p.out_gate != nullptr) p.out_gate[o] = gq;
-    if (p.out_up != nullptr) p.out_up[o] = uq;
-    p.h[o] = hq;
   }
 }
 
@@ -379,6 +433,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams 
 }
 
 constexpr bool routed_kind(int kind) { return kind == K_IQ3_S || kind == K_Q2_0; }
+constexpr bool routed_linear(int kind) { return kind == K_Q4_K || kind == K_Q6_K || kind == K_Q8_0; }
 
 // Whether routed_down_kernel takes a routed one-matrix call: IQ3_S or Q2_0 rows of 1536 or 2560 inputs, float16
 // in and out (the caller has checked the dtypes).
@@ -425,27 +480,68 @@ int launch_routed_down(const MatvecParams& mp, hipStream_t s) {
   }
 }
 
-// Whether routed_glu_kernel takes a paired gate/up call: IQ3_S or Q2_0 rows of 4096 inputs, at most eight
-// tokens, float16 in and out (the caller has checked the dtypes).
+// Whether routed_glu_kernel takes a paired gate/up call: IQ3_S and Q2_0 rows of 4096 inputs at up to eight
+// tokens, float16 in and out (the caller has checked the dtypes). The linear types' gate/up (a shared expert's:
+// 1536 units, under a round of waves) run 5 % faster on direct_decode_kernel, which spreads them over every CU.
 template <int KIND>
 bool routed_glu_takes(const MatvecParams& p) {
-  return routed_kind(KIND) && p.mode == MODE_EXPERT && p.cols == 4096 && p.glu_out != nullptr &&
-         p.pairs / p.share <= kGluMaxTokens && p.experts <= INT32_MAX && (int64_t)p.pairs * p.rows <= INT32_MAX / 2;
+  const int tokens = p.share > 0 ? p.pairs / p.share : 0;
+  return routed_kind(KIND) && tokens <= kGluMaxTokens && p.mode == MODE_EXPERT && p.cols == 4096 &&
+         p.glu_out != nullptr && p.experts <= INT32_MAX && (int64_t)p.pairs * p.rows <= INT32_MAX / 2;
 }
 
-template <int KIND, bool MULTI>
+// Whether routed_glu_kernel's one-matrix form takes a dense matvec: Q4_K rows of 4096 inputs, at least 32768 of
+// them (an lm_head: 151936 rows in 77 us against 98 us on direct_decode_kernel), one token, every row, float16 in
+// and out. At 4096-12288 rows, and for Q6_K (one unit's fields in registers at a time) and Q8_0, the direct
+// kernel is as fast or faster (Q6_K lm_head 125 against 143 us).
+template <int KIND>
+bool routed_one_takes(const MatvecParams& p) {
+  return KIND == K_Q4_K && p.mode == MODE_DENSE && p.cols == 4096 && p.rows >= 32768 && p.tokens == 1 &&
+         p.row_ids == nullptr && p.rows <= INT32_MAX / 2;
+}
+
+template <int KIND, int MODE>
 int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
   const dim3 block(kGluThreads);
   switch (upw) {
-    case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MULTI>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((routed_glu_kernel<KIND, 3, MULTI>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((routed_glu_kernel<KIND, 4, MULTI>), grid, block, 0, s, p); break;
-    case 6: hipLaunchKernelGGL((routed_glu_kernel<KIND, 6, MULTI>), grid, block, 0, s, p); break;
-    case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MULTI>), grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MULTI>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MODE>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((routed_glu_kernel<KIND, 2, MODE>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((routed_glu_kernel<KIND, 3, MODE>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((routed_glu_kernel<KIND, 4, MODE>), grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL((routed_glu_kernel<KIND, 6, MODE>), grid, block, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((routed_glu_kernel<KIND, 8, MODE>), grid, block, 0, s, p); break;
+    case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MODE>), grid, block, 0, s, p); break;
+    case 16: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MODE>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 24, MODE>), grid, block, 0, s, p); break;
   }
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
+}
+
+// Units a wave: the fewest of the forms built that fit the units into one round of resident waves (IQ3_S at two,
+// eight and 24 units spills registers: three, twelve and 16 instead); at most 24, more waves beyond.
+template <int KIND>
+int glu_units_a_wave(int64_t units) {
+  const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * kGluWaves;
+  const int64_t need = (units + capacity - 1) / capacity;
+  static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 16, 24};
+  for (int f : kForms) {
+    if (KIND == K_IQ3_S && (f == 2 || f == 8 || f == 24)) continue;
+    if (f >= need) return f;
+  }
+  return KIND == K_IQ3_S ? 16 : 24;
+}
+
+template <int KIND, int MODE>
+int launch_glu_mode(GluParams& p, hipStream_t s) {
+  const int64_t units = (int64_t)p.na * p.nb;
+  const int upw = glu_units_a_wave<KIND>(units);
+  const int64_t waves = ((units + upw - 1) / upw + kGluWaves - 1) / kGluWaves * kGluWaves;
+  if (waves > INT32_MAX) return STRATA_ERR_SHAPE;
+  p.waves = (int)waves;
+  p.wave_a = p.waves / p.nb;
+  p.wave_b = p.waves % p.nb;
+  return launch_glu_upw<KIND, MODE>(p, upw, dim3((unsigned)(waves / kGluWaves)), s);
 }
 
 template <int KIND>
@@ -468,27 +564,34 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
     p.pairs = mp.pairs;
     p.share = mp.share;
     p.tokens = mp.pairs / mp.share;
-    const bool multi = p.tokens > 1;
-    p.na = multi ? p.rows : p.pairs;
-    p.nb = multi ? p.pairs : p.rows;
-    const int units = p.pairs * p.rows;
-    const int capacity = device_cus() * kGluGroupsPerCU * kGluWaves;
-    int need = (units + capacity - 1) / capacity;
-    // the forms built (two and eight units a wave spill a few registers in IQ3_S)
-    static const int kForms[] = {1, 3, 4, 6, 12, 16};
-    int upw = kGluMaxUnits;
-    for (int f : kForms)
-      if (f >= need) {
-        upw = f;
-        break;
-      }
-    const int64_t waves = ((int64_t)(units + upw - 1) / upw + kGluWaves - 1) / kGluWaves * kGluWaves;
-    if (waves / kGluWaves > INT32_MAX) return STRATA_ERR_SHAPE;
-    p.waves = (int)waves;
-    p.wave_a = p.waves / p.nb;
-    p.wave_b = p.waves % p.nb;
-    const dim3 grid((unsigned)(waves / kGluWaves));
-    return multi ? launch_glu_upw<KIND, true>(p, upw, grid, s) : launch_glu_upw<KIND, false>(p, upw, grid, s);
+    if (p.tokens > 1) {
+      p.na = p.rows;
+      p.nb = p.pairs;
+      return launch_glu_mode<KIND, GLUN>(p, s);
+    }
+    p.na = p.pairs;
+    p.nb = p.rows;
+    return launch_glu_mode<KIND, GLU1>(p, s);
+  }
+}
+
+template <int KIND>
+int launch_routed_one(const MatvecParams& mp, hipStream_t s) {
+  if constexpr (KIND != K_Q4_K) {
+    return STRATA_ERR_SHAPE;
+  } else {
+    GluParams p = {};
+    p.gate = mp.blocks[0];
+    p.x = reinterpret_cast<const u32x4*>(mp.x);
+    p.out_gate = reinterpret_cast<f16*>(mp.out[0]);
+    p.row_bytes = mp.row_bytes;
+    p.rows = mp.rows;
+    p.pairs = 1;
+    p.share = 1;
+    p.tokens = 1;
+    p.na = 1;
+    p.nb = (mp.rows + 1) / 2;
+    return launch_glu_mode<KIND, ONE>(p, s);
   }
 }
 

@@ -114,6 +114,45 @@ def tiled_chunk(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.
     return c[:tokens].to(x.dtype)
 
 
+class FusedLinear(BlockLinear):
+    """Several layers of one block type that read the same input (q, k and v; a shared expert's gate and up) kept
+    as one matrix: their rows one after another, so a token's products are one launch (one kernel's fixed cost
+    in place of one a layer). Called like the layers it fuses, it returns their outputs in order. No counterpart in
+    the reference, whose engine calls the layers one by one (dense.py:109-167, 205-242); the products are the
+    layers' own."""
+
+    def __init__(self, layers):
+        layers = list(layers)
+        first = layers[0]
+        if any(l.kind != first.kind or l.input_dims != first.input_dims or l.to_file is not None or l.planes is not None
+               for l in layers):
+            raise ValueError("fused layers share one block type and input width, as the file's blocks")
+        self.sizes = [l.output_dims for l in layers]
+        rb = B.row_bytes(first.kind, first.input_dims)
+        blocks = torch.cat([l.blocks[:l.output_dims * rb] for l in layers])
+        super().__init__(blocks, first.kind, (sum(self.sizes), first.input_dims))
+
+    def __call__(self, x: torch.Tensor, row_ids=None):
+        if row_ids is not None:
+            raise ValueError("a fused layer takes every row")
+        return tuple(torch.split(super().__call__(x), self.sizes, dim=-1))
+
+
+def gate_up_swiglu(gate: BlockLinear, up: BlockLinear, x: torch.Tensor) -> tuple:
+    """A dense (shared) expert's gate and up at the same tokens, with silu(gate) * up rounded as mlx-lm rounds it,
+    in one launch: (gate . x, up . x, h), each (tokens, rows). The layers are read as one-expert stacks."""
+    if (gate.kind, gate.output_dims, gate.input_dims) != (up.kind, up.output_dims, up.input_dims):
+        raise ValueError("gate and up differ in type or shape")
+    if gate.blocks is None or up.blocks is None or gate.to_file is not None or up.to_file is not None:
+        raise ValueError("gate_up_swiglu takes layers kept as the file's blocks, inputs in the file's order")
+    shape = (1, gate.output_dims, gate.input_dims)
+    g = B.BlockSwitchLinear(gate.blocks, gate.kind, shape)
+    u = B.BlockSwitchLinear(up.blocks, up.kind, shape)
+    x2 = x.reshape(-1, gate.input_dims)
+    idx = torch.zeros(x2.shape[0], dtype=torch.int32, device=x.device)
+    return B.gate_up_swiglu(g, u, x2, idx, 1)
+
+
 class ScaledLinear(BlockLinear):
     """A Q6_K layer given as codes, scales and d (strata_mlx/dense.py:109-167), kept as the file's Q6_K blocks.
     d_step (weights to a d) must be 256: layers whose inputs were reordered are BlockLinear with `inputs`."""

@@ -134,3 +134,59 @@ def test_gate_up_tokens(gpu, kind, tokens, k, rows):
     # the sigmoid's exp is float32 expf on the GPU and float64 in the oracle: where the float16 sigmoid lands on
     # the other side of a rounding boundary, g * sig and its product with u each move by up to one more step
     assert steps.max() <= 2.0 and np.mean(steps > 1.0) <= 1e-3
+
+
+# one token through the dense launches: the linear types at an odd row count and at 4096 rows, and q, k and v
+# fused into one launch (FusedLinear), whose outputs are the separate layers' bits
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("rows", [1537, 4096])
+def test_dense_one_token(gpu, kind, rows):
+    from strata_mlx_amd import dense as D
+    g = torch.Generator(device=gpu).manual_seed(rows)
+    blocks = synth.random_stack(kind, rows * H, gpu, g)
+    x = (np.random.default_rng(rows).standard_normal((1, H)) / 8).astype(np.float16)
+    y = B.window_matvec(blocks, kind, rows, H, torch.from_numpy(x).to(gpu)).float().cpu().numpy()
+    w = O.dequantize(blocks.cpu().numpy(), kind, (rows, H)).astype(np.float64)
+    assert rel_l2(y[0], w @ x[0].astype(np.float64)) <= REL
+    lin = D.BlockLinear(blocks, kind, (rows, H))
+    assert torch.equal(lin(torch.from_numpy(x).to(gpu)).float().cpu(), torch.from_numpy(y))
+
+
+@pytest.mark.parametrize("kind", ["Q6_K", "Q4_K"])
+def test_fused_layers(gpu, kind):
+    from strata_mlx_amd import dense as D
+    g = torch.Generator(device=gpu).manual_seed(9)
+    sizes = (4096, 1024, 1024) if kind == "Q6_K" else (1536, 1536)
+    layers = [D.BlockLinear(synth.random_stack(kind, r * H, gpu, g), kind, (r, H)) for r in sizes]
+    x = (torch.randn((1, H), generator=g, device=gpu) / 8).half()
+    fused = D.FusedLinear(layers)(x)
+    for f, lay in zip(fused, layers):
+        assert torch.equal(f, lay(x))
+    if kind == "Q4_K":  # the shared expert's gate and up with the SwiGLU in one launch
+        gk, uk, hk = (t.float().cpu().numpy() for t in D.gate_up_swiglu(layers[0], layers[1], x))
+        xd = x.float().cpu().numpy().astype(np.float64)[0]
+        for got, lay in ((gk, layers[0]), (uk, layers[1])):
+            w = O.dequantize(lay.blocks.cpu().numpy(), kind, (lay.output_dims, H)).astype(np.float64)
+            assert rel_l2(got[0], w @ xd) <= REL
+        assert torch.equal(torch.from_numpy(gk).half(), fused[0].cpu()) and torch.equal(torch.from_numpy(uk).half(),
+                                                                                       fused[1].cpu())
+        want = O.swiglu_rounded(gk, uk, np.float16).astype(np.float64)
+        steps = np.abs(hk - want) / np.maximum(np.spacing(np.abs(want.astype(np.float16))).astype(np.float64),
+                                               2.0 ** -24)
+        assert steps.max() <= 2.0
+
+
+def test_q4_k_lm_head_one_matrix_form(gpu):
+    """Q4_K rows of 4096 inputs from 32768 rows take the one-matrix form (rows 2i and 2i + 1 a unit): 40000 rows (an
+    odd unit count) against the oracle on a sample of rows."""
+    rows, kind = 40001, "Q4_K"
+    g = torch.Generator(device=gpu).manual_seed(3)
+    blocks = synth.random_stack(kind, rows * H, gpu, g)
+    x = (np.random.default_rng(3).standard_normal((1, H)) / 8).astype(np.float16)
+    y = B.window_matvec(blocks, kind, rows, H, torch.from_numpy(x).to(gpu)).float().cpu().numpy()[0]
+    rb = B.row_bytes(kind, H)
+    at = np.sort(np.random.default_rng(4).choice(rows, 600, replace=False))
+    at[-1] = rows - 1
+    raw = blocks.reshape(rows, rb)[torch.from_numpy(at).to(gpu)].cpu().numpy()
+    w = O.dequantize(raw.reshape(-1), kind, (len(at), H)).astype(np.float64)
+    assert rel_l2(y[at], w @ x[0].astype(np.float64)) <= REL
