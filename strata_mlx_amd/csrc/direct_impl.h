@@ -1306,6 +1306,9 @@ namespace strata_mv {
 // direct kernel, else the persistent wave kernel, else the staged fast kernel; other cases the generic kernels.
 template <int KIND>
 int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int grid_y, int grid_z, hipStream_t s) {
+  // a float32 token against Q4_K rows of 4096 inputs: the persistent form, the token in two float16 parts
+  if (!glu && x_dtype == DT_F32 && out_dtype == DT_F32 && routed_one32_takes<KIND>(p))
+    return launch_routed_one<KIND, true>(p, s);
   if constexpr (DirectKind<KIND>::linear) {  // float16 in and out, rows of run pairs: the direct kernel
     // listed rows too (dense), when the matrix's byte offsets fit 32 bits: a listed row gets the bits of its
     // layer's full product

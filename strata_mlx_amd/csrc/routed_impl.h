@@ -67,6 +67,19 @@ struct Routed {
     }
     return s;
   }
+  // the same against x_a + x_b (a float32 token as two float16 parts): each run decoded once
+  static __device__ __forceinline__ float pair_sum2(const Fields& f, int j, const uint32_t* xa, const uint32_t* xb,
+                                                    const u32x2* tab) {
+    const DirectTables<KIND>& t = *reinterpret_cast<const DirectTables<KIND>*>(tab);
+    float s = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w[16];
+      const RunScale rs = decode_run<KIND>(f, h, j, w, t);
+      s += apply_run<KIND>(rs, w, xa + 16 * h) + apply_run<KIND>(rs, w, xb + 16 * h);
+    }
+    return s;
+  }
 };
 
 template <>
@@ -175,14 +188,15 @@ struct Routed<K_Q2_0> {
 };
 
 // GLU1: gate and up of one token (a unit: row r of each); GLUN: the same at several tokens, in LDS; ONE: one
-// matrix and one token, no routing (a unit: rows 2 i and 2 i + 1).
-enum GluMode : int { GLU1 = 0, GLUN = 1, ONE = 2 };
+// matrix and one token, no routing (a unit: rows 2 i and 2 i + 1); ONE32: ONE with a float32 token and float32
+// products (the token scaled by a power of two into float16 and split into two float16 parts, x = hi + lo).
+enum GluMode : int { GLU1 = 0, GLUN = 1, ONE = 2, ONE32 = 3 };
 
 struct GluParams {
   const uint8_t* gate;  // ONE: the matrix
   const uint8_t* up;
   const uint32_t* idx;  // expert of each pair (ONE: none)
-  const u32x4* x;       // the tokens: 4096 float16 each, as 512 pieces of 16 bytes
+  const u32x4* x;       // the tokens: 4096 float16 each, as 512 pieces of 16 bytes (ONE32: 4096 float32, 1024)
   f16* out_gate;        // gate . x (may be null); ONE: the product
   f16* out_up;          // up . x (may be null)
   f16* h;               // silu(gate . x) * (up . x)
@@ -202,13 +216,19 @@ __device__ __forceinline__ int x_piece_slot(int c) { return glu_x_slot(c >> 3, c
 
 // The unit's two rows decoded and multiplied (gate and up, or rows 2 i and 2 i + 1), and their sums met over the
 // wave: the first row's total and the second's, the same in every lane (read into scalars).
-template <int KIND>
+template <int KIND, bool TWO = false>
 __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], int lane, const uint32_t* x,
-                                         const u32x2* tab, float& gate, float& up) {
+                                         const uint32_t* x2, const u32x2* tab, float& gate, float& up) {
   opaque(f[0]);  // nothing of the decode is done before the workgroup barrier (it would wait for these rows there)
   opaque(f[1]);
-  float g = Routed<KIND>::pair_sum(f[0], lane, x, tab);
-  float u = Routed<KIND>::pair_sum(f[1], lane, x, tab);
+  float g, u;
+  if constexpr (TWO) {
+    g = Routed<KIND>::pair_sum2(f[0], lane, x, x2, tab);
+    u = Routed<KIND>::pair_sum2(f[1], lane, x, x2, tab);
+  } else {
+    g = Routed<KIND>::pair_sum(f[0], lane, x, tab);
+    u = Routed<KIND>::pair_sum(f[1], lane, x, tab);
+  }
   // lanes 0-31 the first row's partial sums two at a time, lanes 32-63 the second's; then within the halves
   float v = sum_swapped(g, u, 32);
   v = sum_swapped(v, v, 16);
@@ -224,19 +244,24 @@ template <int KIND, int UPW, int MODE>
 __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p) {
   typedef Routed<KIND> R;
   typedef typename R::Fields Fields;
-  constexpr int kBuffers = UPW < R::kBuffers ? UPW : R::kBuffers;  // units whose rows are in registers at once
-  constexpr int kTokens = MODE == GLUN ? kGluMaxTokens : 1;
+  constexpr bool kOne = MODE == ONE || MODE == ONE32;
+  constexpr int kMaxBuffers = MODE == ONE32 ? 1 : R::kBuffers;  // ONE32 holds two parts of the token
+  constexpr int kBuffers = UPW < kMaxBuffers ? UPW : kMaxBuffers;  // units whose rows are in registers at once
+  constexpr int kTokens = MODE == GLUN ? kGluMaxTokens : MODE == ONE32 ? 2 : 1;
   __shared__ u32x2 tab[R::kEntries];
   __shared__ u32x4 xs[512 * kTokens];
   const int tid = threadIdx.x, lane = tid & 63;
   const int gw = blockIdx.x * kGluWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // what the workgroup shares, asked for first: the table entry this thread expands and pieces of the tokens
+  // (ONE32: a quarter of a float32 piece, four values, a thread)
   const uint64_t entry = R::fetch(tid);
-  constexpr int kPieceLoads = (512 * kTokens + kGluThreads - 1) / kGluThreads;
+  constexpr int kPieceLoads = MODE == ONE32 ? 1 : (512 * kTokens + kGluThreads - 1) / kGluThreads;
   u32x4 xpiece[kPieceLoads];
 #pragma unroll
-  for (int k = 0; k < kPieceLoads; ++k) xpiece[k] = p.x[min(tid + k * kGluThreads, 512 * p.tokens - 1)];
+  for (int k = 0; k < kPieceLoads; ++k)
+    xpiece[k] = p.x[MODE == ONE32 ? tid : min(tid + k * kGluThreads, 512 * p.tokens - 1)];
+  __shared__ uint32_t wmax[kGluWaves];
 
   // the wave's units (pair, row) and whether each is live; ONE: row is the unit's first row (2 i), pair 0
   int pair[UPW], row[UPW];
@@ -247,7 +272,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
     for (int k = 0; k < UPW; ++k) {
       live[k] = a < p.na;
       const int pr = MODE == GLUN ? b : a, r = MODE == GLUN ? a : b;
-      if constexpr (MODE == ONE) {
+      if constexpr (kOne) {
         pair[k] = 0;
         row[k] = live[k] ? 2 * b : 0;  // past the last unit: the first rows again, nothing written
       } else {
@@ -266,7 +291,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   bool bad[UPW];
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    if constexpr (MODE == ONE) {
+    if constexpr (kOne) {
       bad[k] = false;
       expert[k] = 0u;
     } else {
@@ -276,7 +301,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
     }
   }
   auto issue = [&](int k, Fields(&f)[2]) {
-    if constexpr (MODE == ONE) {
+    if constexpr (kOne) {
       const uint8_t* r0 = p.gate + (int64_t)row[k] * p.row_bytes;
       R::load(r0, lane, f[0]);
       R::load(row[k] + 1 < p.rows ? r0 + p.row_bytes : r0, lane, f[1]);  // an odd last row: the same row twice
@@ -289,15 +314,45 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   };
 
   R::fill(tab, tid, entry);
+  int ex = 0;  // ONE32: the token was divided by 2^ex
+  if constexpr (MODE == ONE32) {
+    // the token's largest magnitude over the workgroup, then the power of two that puts it in [2^14, 2^15)
+    uint32_t m = 0;
 #pragma unroll
-  for (int k = 0; k < kPieceLoads; ++k) {
-    const int c = min(tid + k * kGluThreads, 512 * p.tokens - 1);  // threads past the pieces write one again
-    xs[(c >> 9) * 512 + x_piece_slot(c & 511)] = xpiece[k];
+    for (int i = 0; i < 4; ++i) m = max(m, xpiece[0][i] & 0x7fffffffu);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, d));
+    if (lane == 0) wmax[tid >> 6] = m;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kGluWaves; ++w) m = max(m, wmax[w]);
+    ex = row_exponent(m);
+    // the four values as hi = float16(v / 2^ex) and lo = float16(v / 2^ex - hi): half of float16 piece tid / 2
+    uint32_t hi[2], lo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float a = __builtin_ldexpf(__uint_as_float(xpiece[0][2 * i]), -ex);
+      const float b = __builtin_ldexpf(__uint_as_float(xpiece[0][2 * i + 1]), -ex);
+      const f16 ha = from_f32<f16>(a), hb = from_f32<f16>(b);
+      const f16 la = from_f32<f16>(a - (float)ha), lb = from_f32<f16>(b - (float)hb);
+      hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+      lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+    }
+    u32x2* h2 = reinterpret_cast<u32x2*>(xs + x_piece_slot(tid >> 1)) + (tid & 1);
+    u32x2* l2 = reinterpret_cast<u32x2*>(xs + 512 + x_piece_slot(tid >> 1)) + (tid & 1);
+    *h2 = u32x2{hi[0], hi[1]};
+    *l2 = u32x2{lo[0], lo[1]};
+  } else {
+#pragma unroll
+    for (int k = 0; k < kPieceLoads; ++k) {
+      const int c = min(tid + k * kGluThreads, 512 * p.tokens - 1);  // threads past the pieces write one again
+      xs[(c >> 9) * 512 + x_piece_slot(c & 511)] = xpiece[k];
+    }
   }
   __syncthreads();
   // lane j's activations: the 32 columns of each of its two runs
-  uint32_t x[32];
-  auto read_x = [&](int t) {
+  uint32_t x[32], x2[MODE == ONE32 ? 32 : 1];
+  auto read_x = [&](int t, uint32_t* dst) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int r = run_of<KIND>(lane, h);
@@ -305,11 +360,12 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
       for (int v = 0; v < 4; ++v) {
         const u32x4 c = xs[t * 512 + x_piece_slot(4 * r + v)];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[16 * h + 4 * v + i] = c[i];
+        for (int i = 0; i < 4; ++i) dst[16 * h + 4 * v + i] = c[i];
       }
     }
   };
-  if constexpr (MODE != GLUN) read_x(0);
+  if constexpr (MODE != GLUN) read_x(0, x);
+  if constexpr (MODE == ONE32) read_x(1, x2);
   Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
@@ -318,9 +374,9 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   float gv = 0.0f, uv = 0.0f;
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    if constexpr (MODE == GLUN) read_x(pair[k] / p.share);
+    if constexpr (MODE == GLUN) read_x(pair[k] / p.share, x);
     float g, u;
-    glu_unit<KIND>(f[k % kBuffers], lane, x, tab, g, u);
+    glu_unit<KIND, MODE == ONE32>(f[k % kBuffers], lane, x, x2, tab, g, u);
     if (k + kBuffers < UPW) issue(k + kBuffers, f[k % kBuffers]);
     gv = lane == k ? g : gv;
     uv = lane == k ? u : uv;
@@ -339,7 +395,11 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
     }
   }
   if (lane < UPW && w_live) {
-    if constexpr (MODE == ONE) {
+    if constexpr (MODE == ONE32) {
+      float* out = reinterpret_cast<float*>(p.out_gate);
+      out[w_row] = __builtin_ldexpf(gv, ex);
+      if (w_row + 1 < p.rows) out[w_row + 1] = __builtin_ldexpf(uv, ex);
+    } else if constexpr (MODE == ONE) {
       p.out_gate[w_row] = from_f32<f16>(gv);
       if (w_row + 1 < p.rows) p.out_gate[w_row + 1] = from_f32<f16>(uv);
     } else {
@@ -575,7 +635,15 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
   }
 }
 
+// Whether the float32 form (ONE32) takes a dense matvec: Q4_K rows of 4096 inputs, one float32 token, float32
+// out, every row.
 template <int KIND>
+bool routed_one32_takes(const MatvecParams& p) {
+  return KIND == K_Q4_K && p.mode == MODE_DENSE && p.cols == 4096 && p.tokens == 1 && p.row_ids == nullptr &&
+         p.rows <= INT32_MAX / 2;
+}
+
+template <int KIND, bool F32 = false>
 int launch_routed_one(const MatvecParams& mp, hipStream_t s) {
   if constexpr (KIND != K_Q4_K) {
     return STRATA_ERR_SHAPE;
@@ -591,7 +659,7 @@ int launch_routed_one(const MatvecParams& mp, hipStream_t s) {
     p.tokens = 1;
     p.na = 1;
     p.nb = (mp.rows + 1) / 2;
-    return launch_glu_mode<KIND, ONE>(p, s);
+    return F32 ? launch_glu_mode<KIND, ONE32>(p, s) : launch_glu_mode<KIND, ONE>(p, s);
   }
 }
 
