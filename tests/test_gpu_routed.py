@@ -190,3 +190,22 @@ def test_q4_k_lm_head_one_matrix_form(gpu):
     raw = blocks.reshape(rows, rb)[torch.from_numpy(at).to(gpu)].cpu().numpy()
     w = O.dequantize(raw.reshape(-1), kind, (len(at), H)).astype(np.float64)
     assert rel_l2(y[at], w @ x[0].astype(np.float64)) <= REL
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1.0, 1e6, 1e30])
+def test_q4_k_float32_token_any_range(gpu, scale):
+    """A float32 token against Q4_K rows of 4096 inputs takes the persistent form, which scales the token by a power
+    of two into float16 and splits it into two float16 parts: exact products to about 2^-22 of the largest input,
+    whatever the token's range (beyond float16's, and below its normal numbers)."""
+    rows, kind = 1000, "Q4_K"
+    g = torch.Generator(device=gpu).manual_seed(5)
+    blocks = synth.random_stack(kind, rows * H, gpu, g)
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((1, H)) * scale).astype(np.float32)
+    x[0, :64] *= 1e-4  # a stretch of much smaller values
+    y = B.window_matvec(blocks, kind, rows, H, torch.from_numpy(x).to(gpu)).cpu().numpy()[0]
+    assert y.dtype == np.float32
+    w = O.dequantize(blocks.cpu().numpy(), kind, (rows, H)).astype(np.float64)
+    want = w @ x[0].astype(np.float64)
+    assert rel_l2(y, want) <= 1e-5
+    assert np.abs(y - want).max() <= 1e-5 * np.abs(w).max() * np.abs(x).max() * np.sqrt(H)
