@@ -28,10 +28,9 @@
 // gate row's partial sums and the up row's meet in one exchange of halves and then within the halves.
 //
 // Several tokens (pairs / share of them, up to 8): every pair is its own unit, and the tokens sit in LDS beside
-// the codebook; a unit reads its token's 128 bytes a lane from there. Units run row by row over all pairs, so the
-// pairs naming one expert read each of its rows at about the same time, and the second read finds the bytes in a
-// cache. Q2_0 takes the same kernels with a 256-entry table of a code byte's four weights (c - 1) in place of the
-// codebook, and d for a lane's block.
+// the codebook; a wave's units are consecutive rows of a pair, and it reads its token's 128 bytes a lane from LDS
+// once a pair. Q2_0 takes the same kernels with a 256-entry table of a code byte's four weights (c - 1) in place
+// of the codebook, and d for a lane's block.
 #pragma once
 // Included by direct_impl.h ahead of the dispatch (it uses that file's fields, offsets and reductions).
 
@@ -267,11 +266,13 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   int pair[UPW], row[UPW];
   bool live[UPW];
   {
-    int a = gw / p.nb, b = gw - a * p.nb;
+    // GLUN: a wave's units consecutive, pair by pair (its token read once a pair); else gw, gw + waves, ...
+    const int u0 = MODE == GLUN ? gw * UPW : gw;
+    int a = u0 / p.nb, b = u0 - a * p.nb;
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
       live[k] = a < p.na;
-      const int pr = MODE == GLUN ? b : a, r = MODE == GLUN ? a : b;
+      const int pr = a, r = b;
       if constexpr (kOne) {
         pair[k] = 0;
         row[k] = live[k] ? 2 * b : 0;  // past the last unit: the first rows again, nothing written
@@ -279,8 +280,8 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
         pair[k] = live[k] ? pr : p.pairs - 1;  // past the last unit: the last pair's last row again, nothing written
         row[k] = live[k] ? r : p.rows - 1;
       }
-      b += p.wave_b;
-      a += p.wave_a;
+      b += MODE == GLUN ? 1 : p.wave_b;
+      a += MODE == GLUN ? 0 : p.wave_a;
       if (b >= p.nb) {
         b -= p.nb;
         ++a;
@@ -374,7 +375,9 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p)
   float gv = 0.0f, uv = 0.0f;
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    if constexpr (MODE == GLUN) read_x(pair[k] / p.share, x);
+    if constexpr (MODE == GLUN) {
+      if (k == 0 || pair[k] != pair[k - 1]) read_x(pair[k] / p.share, x);
+    }
     float g, u;
     glu_unit<KIND, MODE == ONE32>(f[k % kBuffers], lane, x, x2, tab, g, u);
     if (k + kBuffers < UPW) issue(k + kBuffers, f[k % kBuffers]);
@@ -625,8 +628,8 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
     p.share = mp.share;
     p.tokens = mp.pairs / mp.share;
     if (p.tokens > 1) {
-      p.na = p.rows;
-      p.nb = p.pairs;
+      p.na = p.pairs;
+      p.nb = p.rows;
       return launch_glu_mode<KIND, GLUN>(p, s);
     }
     p.na = p.pairs;
