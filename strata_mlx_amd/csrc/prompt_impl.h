@@ -157,6 +157,41 @@ __device__ __forceinline__ float swiglu_f32(float g, float u) {
   return (g * s) * u;
 }
 
+// lane (n, g) holds slots 4g + j of each tile, for rows row0 and row1
+template <int MODE, typename OT, int NTC>
+__device__ __forceinline__ void write_chunk(const PromptParams& p, const f32x4 (&acc)[2][NTC], int t0, int g,
+                                            int row0, int row1) {
+#pragma unroll
+  for (int i = 0; i < NTC; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int slot = (t0 + i) * 16 + 4 * g + j;
+      float v0 = acc[0][i][j], v1 = acc[1][i][j];
+      if (p.a_max != nullptr) {
+        const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
+        const int ex = row_exponent(p.a_max[r]);
+        v0 = __builtin_ldexpf(v0, ex);
+        v1 = __builtin_ldexpf(v1, ex);
+      }
+      if constexpr (MODE == PM_C32) {
+        float* c = reinterpret_cast<float*>(p.out) + (int64_t)slot * p.rows;
+        if (row0 < p.rows) c[row0] = v0;
+        if (row1 < p.rows) c[row1] = v1;
+      } else if constexpr (MODE == PM_GLU) {
+        if (row0 < p.rows)
+          store_out<OT>(reinterpret_cast<OT*>(p.out) + (int64_t)slot * p.rows + row0, swiglu_f32(v0, v1));
+      } else {
+        const uint32_t pr = p.slot_pair[slot];
+        if (pr != 0xffffffffu) {
+          OT* y = reinterpret_cast<OT*>(p.out) + (int64_t)pr * p.rows;
+          if (row0 < p.rows) store_out<OT>(y + row0, v0);
+          if (row1 < p.rows) store_out<OT>(y + row1, v1);
+        }
+      }
+    }
+  }
+}
+
 // One chunk of exactly NTC tiles (NTC at compile time: no per-tile branches between the MFMAs).
 template <int KIND, int MODE, typename OT, int WAVES, int NTC>
 __device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTables<KIND>& tab,
@@ -271,41 +306,235 @@ __device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTab
     }
   }
 
-  // lane (n, g) holds slots 4g + j of each tile, for rows row0 and row1
+  write_chunk<MODE, OT, NTC>(p, acc, t0, g, row0, row1);
+}
+
+
+// The staged form of run_chunk (IQ3_S, IQ3_XXS): the rows' bytes of a step go to LDS by gfx950's direct loads
+// (global_load_lds_dword: lane l's dword lands at M0 + 4 l), each wave instruction a contiguous 256-byte piece of
+// two or three rows, and each lane reads its fields from there. Loaded straight into registers (run_chunk), each of
+// a lane's field loads touches the cache lines of 16 rows at once, and the texture-address unit and the L1 tag
+// lookups, not HBM, set the pace.
+//
+// A wave stages its own rows: two groups of 16 (SwiGLU form: its gate rows, then its up rows), each row a slot of
+// 112 bytes holding the dwords from the one with the step's first byte to the one with its last (a step of 110 or
+// 98 bytes starts two bytes into a dword at odd steps; rows are whole dwords). Those dwords lie within the stack
+// whenever its base and a row's bytes are multiples of 4 (the launch checks). LDS reads are naturally aligned
+// (16-byte reads at multiples of 16, 8-byte at multiples of 8: misaligned ones run about 14 times slower), and a
+// field that starts 2 or 4 bytes past such a boundary is put together in registers (v_alignbyte).
+//
+// Two buffers: the next step's rows are asked for before this step's are decoded. The loads are inline assembly,
+// so the compiler places no wait of its own for them: the one wait (vmcnt(0)) comes at the top of each step, and
+// the workgroup barriers here wait only for LDS (a __syncthreads would also wait for the next step's rows).
+template <int KIND>
+constexpr bool kStagedKind = KIND == K_IQ3_S || KIND == K_IQ3_XXS;
+template <int KIND>
+constexpr int kStepBytes = KIND == K_IQ3_S ? 110 : 98;
+template <int KIND>
+constexpr int kSlotDwords = (kStepBytes<KIND> + 2) / 4;  // dwords a row's step spans: 28, 25
+constexpr int kSlotPitch = 28;                            // dwords a row's slot (112 bytes)
+constexpr int kGroupLoads = 16 * kSlotPitch / 64;         // wave instructions a group of 16 rows: 7
+constexpr int kGroupBytes = 256 * kGroupLoads;            // a group's buffer
+
+// lane l's dword at base + voff into LDS at lds + 4 l (the wave's LDS address in M0)
+__device__ __forceinline__ void dma_dword(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef uint32_t u32x4a16 __attribute__((ext_vector_type(4), aligned(16)));
+typedef uint32_t u32x2a8 __attribute__((ext_vector_type(2), aligned(8)));
+template <typename T>
+__device__ __forceinline__ T lds_at(const uint8_t* base, uint32_t off) {  // off a multiple of sizeof(T)
+  const __attribute__((address_space(3))) uint8_t* b = (const __attribute__((address_space(3))) uint8_t*)base;
+  return *(const __attribute__((address_space(3))) T*)(b + off);
+}
+// 16 bytes at a0 + SH (a0 a multiple of 16; SH 2 or 4)
+template <int SH>
+__device__ __forceinline__ u32x4 lds_16(const uint8_t* base, uint32_t a0) {
+  const u32x4a16 w = lds_at<u32x4a16>(base, a0);
+  const uint32_t w4 = lds_at<uint32_t>(base, a0 + 16);
+  if constexpr (SH == 4) return u32x4{w[1], w[2], w[3], w4};
+  return u32x4{__builtin_amdgcn_alignbyte(w[1], w[0], SH), __builtin_amdgcn_alignbyte(w[2], w[1], SH),
+               __builtin_amdgcn_alignbyte(w[3], w[2], SH), __builtin_amdgcn_alignbyte(w4, w[3], SH)};
+}
+// 8 bytes at a0 + SH (a0 a multiple of 8; SH 2 or 4)
+template <int SH>
+__device__ __forceinline__ u32x2 lds_8(const uint8_t* base, uint32_t a0) {
+  const u32x2a8 w = lds_at<u32x2a8>(base, a0);
+  const uint32_t w2 = lds_at<uint32_t>(base, a0 + 8);
+  if constexpr (SH == 4) return u32x2{w[1], w2};
+  return u32x2{__builtin_amdgcn_alignbyte(w[1], w[0], SH), __builtin_amdgcn_alignbyte(w2, w[1], SH)};
+}
+// lane g's fields from a staged row slot whose step starts S bytes in (S = 0 or 2): the fields at the offsets of
+// lane_offsets (d @0, qs @2 + 16 g; IQ3_S qh @66 + 2 g, signs @74 + 8 g, scale @106 + 2 (g / 2); IQ3_XXS aux
+// @66 + 8 g)
+template <int KIND, int S>
+__device__ __forceinline__ void lds_fields(const uint8_t* slot, int g, RunPair<KIND>& f) {
+  const uint32_t gg = (uint32_t)g;
+  f.d = lds_at<uint16_t>(slot, S);
+  f.qs = lds_16<S + 2>(slot, 16 * gg);
+  if constexpr (KIND == K_IQ3_S) {
+    f.qh = lds_at<uint16_t>(slot, S + 66 + 2 * gg);
+    f.sg = lds_8<S + 2>(slot, 72 + 8 * gg);
+    f.sc = lds_at<uint16_t>(slot, S + 106 + 2 * (gg >> 1));
+  } else {
+    f.aux = lds_8<S + 2>(slot, 64 + 8 * gg);
+  }
+}
+
+template <int KIND, int MODE, typename OT, int WAVES, int NTC>
+__device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const DirectTables<KIND>& tab,
+                                                 f16* a_lds, uint8_t* w_lds, uint32_t e, int t0, int rb, int tid,
+                                                 int wave) {
+  constexpr int kThreadsWg = 64 * WAVES;
+  constexpr bool kGlu = MODE == PM_GLU;
+  constexpr int kRowsWave = kGlu ? 16 : 32;
+  constexpr int kChunks = NTC * 16 * (kStep / 8);
+  constexpr int kLoads = kChunks / kThreadsWg;
+  static_assert(kChunks % kThreadsWg == 0, "whole pieces a thread");
+  static_assert(kStagedKind<KIND>, "staged rows: IQ3_S, IQ3_XXS");
+  constexpr int kSB = kStepBytes<KIND>, kDW = kSlotDwords<KIND>, kGL = kGroupLoads;
+  const int lane = tid & 63;
+
+  const int n = lane & 15, g = lane >> 4;
+  const int r0 = rb * kRowsWave * WAVES + wave * kRowsWave;
+  const int row0 = r0 + n, row1 = kGlu ? r0 + n : r0 + 16 + n;
+  const uint8_t* mat[2] = {p.blocks[0] + (int64_t)e * p.mat_bytes,
+                           (kGlu ? p.blocks[1] : p.blocks[0]) + (int64_t)e * p.mat_bytes};
+  const int grow[2] = {r0, kGlu ? r0 : r0 + 16};  // first row of each group
+  const int nsteps = p.cols / kStep;
+
+  // the lane's dword of each staging load: row q of the group, dword d of its slot (the slot's spare dwords: the
+  // row's last dword again)
+  uint32_t voff[2][kGL];
 #pragma unroll
-  for (int i = 0; i < NTC; ++i) {
+  for (int grp = 0; grp < 2; ++grp)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int slot = (t0 + i) * 16 + 4 * g + j;
-      float v0 = acc[0][i][j], v1 = acc[1][i][j];
-      if (p.a_max != nullptr) {
-        const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
-        const int ex = row_exponent(p.a_max[r]);
-        v0 = __builtin_ldexpf(v0, ex);
-        v1 = __builtin_ldexpf(v1, ex);
-      }
-      if constexpr (MODE == PM_C32) {
-        float* c = reinterpret_cast<float*>(p.out) + (int64_t)slot * p.rows;
-        if (row0 < p.rows) c[row0] = v0;
-        if (row1 < p.rows) c[row1] = v1;
-      } else if constexpr (MODE == PM_GLU) {
-        if (row0 < p.rows)
-          store_out<OT>(reinterpret_cast<OT*>(p.out) + (int64_t)slot * p.rows + row0, swiglu_f32(v0, v1));
-      } else {
-        const uint32_t pr = p.slot_pair[slot];
-        if (pr != 0xffffffffu) {
-          OT* y = reinterpret_cast<OT*>(p.out) + (int64_t)pr * p.rows;
-          if (row0 < p.rows) store_out<OT>(y + row0, v0);
-          if (row1 < p.rows) store_out<OT>(y + row1, v1);
+    for (int i = 0; i < kGL; ++i) {
+      const int f = 64 * i + lane;
+      const int q = f / kSlotPitch, d = min(f % kSlotPitch, kDW - 1);
+      voff[grp][i] = (uint32_t)min(grow[grp] + q, p.rows - 1) * (uint32_t)p.row_bytes + 4u * (uint32_t)d;
+    }
+  // LDS: [buffer][wave][group] slots
+  const uint32_t w_base = (uint32_t)(uintptr_t)w_lds;
+  auto slot_addr = [&](int buf, int grp) {
+    return w_base + (uint32_t)(((buf * WAVES + wave) * 2 + grp) * kGroupBytes);
+  };
+  auto stage = [&](int k, int buf) {
+    const uint32_t sk = (uint32_t)(k * kSB);
+    const uint32_t first = sk & ~3u;  // the dword holding the step's first byte
+#pragma unroll
+    for (int grp = 0; grp < 2; ++grp) {
+      const uint8_t* base = mat[grp] + first;
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(slot_addr(buf, grp));
+#pragma unroll
+      for (int i = 0; i < kGL; ++i) dma_dword(base, voff[grp][i], dst + 256u * i);
+    }
+  };
+
+  const f16* arow[kLoads];
+  int adst[kLoads];
+#pragma unroll
+  for (int q = 0; q < kLoads; ++q) {
+    const int c = tid + q * kThreadsWg;
+    const int i = c / (16 * (kStep / 8)), m = (c / (kStep / 8)) % 16, piece = c % (kStep / 8);
+    const int slot = (t0 + i) * 16 + m;
+    const uint32_t r = p.a_row ? p.a_row[slot] : (uint32_t)slot;
+    arow[q] = p.a + (int64_t)r * p.cols + 8 * piece;
+    adst[q] = (i * 16 + m) * kPitch + 8 * piece;
+  }
+  u32x4 av[kLoads];
+#pragma unroll
+  for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q]);
+  stage(0, 0);
+
+  f32x4 acc[2][NTC];
+#pragma unroll
+  for (int i = 0; i < NTC; ++i) acc[0][i] = acc[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < nsteps; kb += 2) {
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+      const int k = kb + sp;
+      if (k < nsteps) {
+        wait_loads();   // this wave's rows of step k and its activation pieces
+        lds_barrier();  // every wave has read the last step's activations (and the tables are written)
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+        if (k + 1 < nsteps) {
+          stage(k + 1, sp ^ 1);
+#pragma unroll
+          for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 1) * kStep);
+        }
+        lds_barrier();
+
+        RunPair<KIND> f[2];
+#pragma unroll
+        for (int grp = 0; grp < 2; ++grp) {
+          const uint8_t* slot = reinterpret_cast<const uint8_t*>(w_lds) +
+                                ((sp * WAVES + wave) * 2 + grp) * kGroupBytes + 4 * kSlotPitch * n;
+          if (sp == 0)  // k even: the step starts at a dword; odd: 2 bytes in (kSB is 2 mod 4)
+            lds_fields<KIND, 0>(slot, g, f[grp]);
+          else
+            lds_fields<KIND, 2>(slot, g, f[grp]);
+        }
+
+        f32x4 part[2][NTC];
+#pragma unroll
+        for (int i = 0; i < NTC; ++i) part[0][i] = part[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          f16x8 a8[4][NTC];
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int i = 0; i < NTC; ++i)
+              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
+          uint32_t w0[16], w1[16];
+          decode_folded<KIND>(f[0], h, g, w0, tab);
+          decode_folded<KIND>(f[1], h, g, w1, tab);
+#pragma unroll
+          for (int q = 2; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < NTC; ++i)
+              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[4 * q], w0[4 * q + 1], w0[4 * q + 2], w0[4 * q + 3]});
+            const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[4 * q], w1[4 * q + 1], w1[4 * q + 2], w1[4 * q + 3]});
+#pragma unroll
+            for (int i = 0; i < NTC; ++i) {
+              f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
+              f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
+              p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b0, p0, 0, 0, 0);
+              p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b1, p1, 0, 0, 0);
+            }
+          }
+        }
+        if constexpr (has_step_scale<KIND>()) {
+          const float s0 = step_scale<KIND>(f[0]), s1 = step_scale<KIND>(f[1]);
+#pragma unroll
+          for (int i = 0; i < NTC; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              acc[0][i][j] = __builtin_fmaf(s0, part[0][i][j], acc[0][i][j]);
+              acc[1][i][j] = __builtin_fmaf(s1, part[1][i][j], acc[1][i][j]);
+            }
+          }
         }
       }
     }
   }
+  write_chunk<MODE, OT, NTC>(p, acc, t0, g, row0, row1);
 }
 
-template <int KIND, int MODE, typename OT, int WAVES, int NT>
+template <int KIND, int MODE, typename OT, int WAVES, int NT, bool STAGED>
 __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptParams p) {
   constexpr int kThreadsWg = 64 * WAVES;
+  __shared__ __attribute__((aligned(16))) uint8_t w_lds[STAGED && kStagedKind<KIND> ? 2 * WAVES * 2 * kGroupBytes : 16];
   __shared__ DirectTables<KIND> tab;
   __shared__ __attribute__((aligned(16))) f16 a_lds[NT * 16 * kPitch];
 
@@ -335,10 +564,17 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
     strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
   }
   static_assert(NT == 2, "chunks of one or two tiles");
-  if (nt == 1)
-    run_chunk<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, e, t0, rb, tid, wave);
-  else
-    run_chunk<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, e, t0, rb, tid, wave);
+  if constexpr (STAGED && kStagedKind<KIND>) {
+    if (nt == 1)
+      run_chunk_staged<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
+    else
+      run_chunk_staged<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
+  } else {
+    if (nt == 1)
+      run_chunk<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, e, t0, rb, tid, wave);
+    else
+      run_chunk<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, e, t0, rb, tid, wave);
+  }
 }
 
 template <int MODE>
@@ -353,6 +589,7 @@ inline bool prompt_takes(int kind, int64_t cols) {
 
 constexpr int kWaves = 4;
 constexpr int kTiles = 2;
+constexpr bool kStaged = true;  // rows through LDS by direct loads (run_chunk_staged)
 
 template <int KIND, int MODE, typename OT>
 int launch_prompt(PromptParams& p, hipStream_t s) {
@@ -362,8 +599,15 @@ int launch_prompt(PromptParams& p, hipStream_t s) {
   const int64_t grid = tiles * p.row_blocks;
   if (grid <= 0) return STRATA_OK;
   if (grid > 0x7fffffff) return STRATA_ERR_SHAPE;
-  hipLaunchKernelGGL((prompt_kernel<KIND, MODE, OT, kWaves, kTiles>), dim3((unsigned)grid), dim3(64 * kWaves), 0, s,
-                     p);
+  // staged rows read whole dwords: the stacks' bases and a row's bytes multiples of 4
+  const bool staged = kStaged && kStagedKind<KIND> && ((uintptr_t)p.blocks[0] & 3) == 0 && ((uintptr_t)p.blocks[1] & 3) == 0 &&
+                      p.row_bytes % 4 == 0 && p.mat_bytes % 4 == 0;
+  if (staged)
+    hipLaunchKernelGGL((prompt_kernel<KIND, MODE, OT, kWaves, kTiles, true>), dim3((unsigned)grid), dim3(64 * kWaves),
+                       0, s, p);
+  else
+    hipLaunchKernelGGL((prompt_kernel<KIND, MODE, OT, kWaves, kTiles, false>), dim3((unsigned)grid), dim3(64 * kWaves),
+                       0, s, p);
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }
