@@ -323,9 +323,12 @@ __device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTab
 // (16-byte reads at multiples of 16, 8-byte at multiples of 8: misaligned ones run about 14 times slower), and a
 // field that starts 2 or 4 bytes past such a boundary is put together in registers (v_alignbyte).
 //
-// Two buffers: the next step's rows are asked for before this step's are decoded. The loads are inline assembly,
-// so the compiler places no wait of its own for them: the one wait (vmcnt(0)) comes at the top of each step, and
-// the workgroup barriers here wait only for LDS (a __syncthreads would also wait for the next step's rows).
+// One row buffer a wave: the next step's rows are asked for as soon as this step's fields are in registers, and
+// arrive while they are decoded. Two activation buffers: one workgroup barrier a step. The loads are inline
+// assembly, so the compiler places no wait of its own for them: the one wait (vmcnt(0)) comes at the top of each
+// step, and the barriers wait only for LDS (a __syncthreads would also wait for the next step's rows). The LDS
+// (50-52 KB) and the registers leave three workgroups on a CU; at two (a third row buffer, or the IQ3_XXS codebook
+// with its signs folded in, 32 KB) or at four (128 registers, spilled) the kernel ran slower.
 template <int KIND>
 constexpr bool kStagedKind = KIND == K_IQ3_S || KIND == K_IQ3_XXS;
 template <int KIND>
@@ -385,7 +388,7 @@ __device__ __forceinline__ void lds_fields(const uint8_t* slot, int g, RunPair<K
   }
 }
 
-template <int KIND, int MODE, typename OT, int WAVES, int NTC>
+template <int KIND, int MODE, typename OT, int WAVES, int NT, int NTC>
 __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const DirectTables<KIND>& tab,
                                                  f16* a_lds, uint8_t* w_lds, uint32_t e, int t0, int rb, int tid,
                                                  int wave) {
@@ -397,6 +400,7 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
   static_assert(kChunks % kThreadsWg == 0, "whole pieces a thread");
   static_assert(kStagedKind<KIND>, "staged rows: IQ3_S, IQ3_XXS");
   constexpr int kSB = kStepBytes<KIND>, kDW = kSlotDwords<KIND>, kGL = kGroupLoads;
+  constexpr int kABuf = NT * 16 * kPitch;  // float16: an activation buffer
   const int lane = tid & 63;
 
   const int n = lane & 15, g = lane >> 4;
@@ -418,18 +422,13 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
       const int q = f / kSlotPitch, d = min(f % kSlotPitch, kDW - 1);
       voff[grp][i] = (uint32_t)min(grow[grp] + q, p.rows - 1) * (uint32_t)p.row_bytes + 4u * (uint32_t)d;
     }
-  // LDS: [buffer][wave][group] slots
   const uint32_t w_base = (uint32_t)(uintptr_t)w_lds;
-  auto slot_addr = [&](int buf, int grp) {
-    return w_base + (uint32_t)(((buf * WAVES + wave) * 2 + grp) * kGroupBytes);
-  };
-  auto stage = [&](int k, int buf) {
-    const uint32_t sk = (uint32_t)(k * kSB);
-    const uint32_t first = sk & ~3u;  // the dword holding the step's first byte
+  auto stage = [&](int k) {
+    const uint32_t first = (uint32_t)(k * kSB) & ~3u;  // the dword holding the step's first byte
 #pragma unroll
     for (int grp = 0; grp < 2; ++grp) {
       const uint8_t* base = mat[grp] + first;
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(slot_addr(buf, grp));
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(w_base + (uint32_t)((wave * 2 + grp) * kGroupBytes));
 #pragma unroll
       for (int i = 0; i < kGL; ++i) dma_dword(base, voff[grp][i], dst + 256u * i);
     }
@@ -449,7 +448,13 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
   u32x4 av[kLoads];
 #pragma unroll
   for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q]);
-  stage(0, 0);
+#pragma unroll
+  for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+  stage(0);
+  if (nsteps > 1) {
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + kStep);
+  }
 
   f32x4 acc[2][NTC];
 #pragma unroll
@@ -460,27 +465,31 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
     for (int sp = 0; sp < 2; ++sp) {
       const int k = kb + sp;
       if (k < nsteps) {
-        wait_loads();   // this wave's rows of step k and its activation pieces
-        lds_barrier();  // every wave has read the last step's activations (and the tables are written)
-#pragma unroll
-        for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+        wait_loads();   // this wave's rows of step k and its activation pieces of step k + 1
+        lds_barrier();  // every wave's activations of step k are written and every wave is done with step k - 1
         if (k + 1 < nsteps) {
-          stage(k + 1, sp ^ 1);
 #pragma unroll
-          for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 1) * kStep);
+          for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + (sp ^ 1) * kABuf + adst[q]) = av[q];
         }
-        lds_barrier();
-
         RunPair<KIND> f[2];
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
-          const uint8_t* slot = reinterpret_cast<const uint8_t*>(w_lds) +
-                                ((sp * WAVES + wave) * 2 + grp) * kGroupBytes + 4 * kSlotPitch * n;
+          const uint8_t* slot = reinterpret_cast<const uint8_t*>(w_lds) + (wave * 2 + grp) * kGroupBytes +
+                                4 * kSlotPitch * n;
           if (sp == 0)  // k even: the step starts at a dword; odd: 2 bytes in (kSB is 2 mod 4)
             lds_fields<KIND, 0>(slot, g, f[grp]);
           else
             lds_fields<KIND, 2>(slot, g, f[grp]);
         }
+        if (k + 1 < nsteps) {  // the rows of step k + 1 into the same buffer, once this step's fields are read
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          stage(k + 1);
+        }
+        if (k + 2 < nsteps) {
+#pragma unroll
+          for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 2) * kStep);
+        }
+        const f16* ab = a_lds + sp * kABuf;
 
         f32x4 part[2][NTC];
 #pragma unroll
@@ -492,7 +501,7 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
           for (int q = 0; q < 2; ++q)
 #pragma unroll
             for (int i = 0; i < NTC; ++i)
-              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
+              a8[q][i] = *reinterpret_cast<const f16x8*>(ab + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
           uint32_t w0[16], w1[16];
           decode_folded<KIND>(f[0], h, g, w0, tab);
           decode_folded<KIND>(f[1], h, g, w1, tab);
@@ -500,29 +509,25 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
           for (int q = 2; q < 4; ++q)
 #pragma unroll
             for (int i = 0; i < NTC; ++i)
-              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
+              a8[q][i] = *reinterpret_cast<const f16x8*>(ab + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[4 * q], w0[4 * q + 1], w0[4 * q + 2], w0[4 * q + 3]});
             const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[4 * q], w1[4 * q + 1], w1[4 * q + 2], w1[4 * q + 3]});
 #pragma unroll
             for (int i = 0; i < NTC; ++i) {
-              f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
-              f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
-              p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b0, p0, 0, 0, 0);
-              p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b1, p1, 0, 0, 0);
+              part[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b0, part[0][i], 0, 0, 0);
+              part[1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b1, part[1][i], 0, 0, 0);
             }
           }
         }
-        if constexpr (has_step_scale<KIND>()) {
-          const float s0 = step_scale<KIND>(f[0]), s1 = step_scale<KIND>(f[1]);
+        const float s0 = step_scale<KIND>(f[0]), s1 = step_scale<KIND>(f[1]);
 #pragma unroll
-          for (int i = 0; i < NTC; ++i) {
+        for (int i = 0; i < NTC; ++i) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              acc[0][i][j] = __builtin_fmaf(s0, part[0][i][j], acc[0][i][j]);
-              acc[1][i][j] = __builtin_fmaf(s1, part[1][i][j], acc[1][i][j]);
-            }
+          for (int j = 0; j < 4; ++j) {
+            acc[0][i][j] = __builtin_fmaf(s0, part[0][i][j], acc[0][i][j]);
+            acc[1][i][j] = __builtin_fmaf(s1, part[1][i][j], acc[1][i][j]);
           }
         }
       }
@@ -534,9 +539,10 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
 template <int KIND, int MODE, typename OT, int WAVES, int NT, bool STAGED>
 __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptParams p) {
   constexpr int kThreadsWg = 64 * WAVES;
-  __shared__ __attribute__((aligned(16))) uint8_t w_lds[STAGED && kStagedKind<KIND> ? 2 * WAVES * 2 * kGroupBytes : 16];
+  constexpr bool kStagedHere = STAGED && kStagedKind<KIND>;
+  __shared__ __attribute__((aligned(16))) uint8_t w_lds[kStagedHere ? WAVES * 2 * kGroupBytes : 16];
   __shared__ DirectTables<KIND> tab;
-  __shared__ __attribute__((aligned(16))) f16 a_lds[NT * 16 * kPitch];
+  __shared__ __attribute__((aligned(16))) f16 a_lds[(kStagedHere ? 2 : 1) * NT * 16 * kPitch];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -564,11 +570,11 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
     strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
   }
   static_assert(NT == 2, "chunks of one or two tiles");
-  if constexpr (STAGED && kStagedKind<KIND>) {
+  if constexpr (kStagedHere) {
     if (nt == 1)
-      run_chunk_staged<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
+      run_chunk_staged<KIND, MODE, OT, WAVES, NT, 1>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
     else
-      run_chunk_staged<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
+      run_chunk_staged<KIND, MODE, OT, WAVES, NT, 2>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
   } else {
     if (nt == 1)
       run_chunk<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, e, t0, rb, tid, wave);
