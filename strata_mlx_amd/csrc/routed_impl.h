@@ -38,6 +38,12 @@ namespace strata_mv {
 
 constexpr int kGluThreads = 1024;  // sixteen waves a workgroup, one workgroup a CU
 constexpr int kGluWaves = kGluThreads / 64;
+// Q6_K and Q8_0 (a run pair's fields take 18 registers) at eight waves a workgroup: the registers for three units'
+// rows a wave (at sixteen waves, two units' rows spilled)
+template <int KIND>
+constexpr int glu_threads() {
+  return KIND == K_Q6_K || KIND == K_Q8_0 ? 512 : kGluThreads;
+}
 constexpr int kGluGroupsPerCU = 1;
 constexpr int kGluMaxUnits = 16;   // units a wave (straight-line code); more units: more waves
 constexpr int kGluMaxTokens = 8;   // tokens in LDS
@@ -48,7 +54,7 @@ constexpr int kGluMaxTokens = 8;   // tokens in LDS
 template <int KIND>
 struct Routed {
   static constexpr int kEntries = 1;
-  static constexpr int kBuffers = KIND == K_Q6_K ? 1 : 2;  // Q6_K's 18 registers a run pair spill at two
+  static constexpr int kBuffers = glu_threads<KIND>() < kGluThreads ? 3 : 2;
   typedef RunPair<KIND> Fields;
   static __device__ __forceinline__ uint64_t fetch(int) { return 0; }
   static __device__ __forceinline__ void fill(u32x2*, int, uint64_t) {}
@@ -240,7 +246,8 @@ __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], 
 }
 
 template <int KIND, int UPW, int MODE>
-__global__ __launch_bounds__(kGluThreads, 4) void routed_glu_kernel(GluParams p) {
+__global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) void routed_glu_kernel(GluParams p) {
+  constexpr int kGluThreads = glu_threads<KIND>(), kGluWaves = kGluThreads / 64;
   typedef Routed<KIND> R;
   typedef typename R::Fields Fields;
   constexpr bool kOne = MODE == ONE || MODE == ONE32;
@@ -553,19 +560,21 @@ bool routed_glu_takes(const MatvecParams& p) {
          p.glu_out != nullptr && p.experts <= INT32_MAX && (int64_t)p.pairs * p.rows <= INT32_MAX / 2;
 }
 
-// Whether routed_glu_kernel's one-matrix form takes a dense matvec: Q4_K rows of 4096 inputs, at least 32768 of
-// them (an lm_head: 151936 rows in 77 us against 98 us on direct_decode_kernel), one token, every row, float16 in
-// and out. At 4096-12288 rows, and for Q6_K (one unit's fields in registers at a time) and Q8_0, the direct
-// kernel is as fast or faster (Q6_K lm_head 125 against 143 us).
+// Whether routed_glu_kernel's one-matrix form takes a dense matvec: rows of 4096 inputs, one token, every row,
+// float16 in and out; Q4_K at 32768 rows or more (an lm_head: 151936 rows in 77 us against 98 us on
+// direct_decode_kernel), Q6_K and Q8_0 at up to 16384 (4096 rows: 6.4 against 7.9 us for Q6_K, 6.5 against 8.2 us
+// for Q8_0; q, k and v as one 12288-row launch: 13.6 against 14.0 us). Below 32768 rows Q4_K, and above 16384 Q6_K
+// (lm_head: 138 against 125 us), run faster on the direct kernel.
 template <int KIND>
 bool routed_one_takes(const MatvecParams& p) {
-  return KIND == K_Q4_K && p.mode == MODE_DENSE && p.cols == 4096 && p.rows >= 32768 && p.tokens == 1 &&
-         p.row_ids == nullptr && p.rows <= INT32_MAX / 2;
+  const bool kind = (KIND == K_Q4_K && p.rows >= 32768) || ((KIND == K_Q6_K || KIND == K_Q8_0) && p.rows <= 16384);
+  return kind && p.mode == MODE_DENSE && p.cols == 4096 && p.tokens == 1 && p.row_ids == nullptr &&
+         p.rows <= INT32_MAX / 2;
 }
 
 template <int KIND, int MODE>
 int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
-  const dim3 block(kGluThreads);
+  const dim3 block(glu_threads<KIND>());
   switch (upw) {
     case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MODE>), grid, block, 0, s, p); break;
     case 2: hipLaunchKernelGGL((routed_glu_kernel<KIND, 2, MODE>), grid, block, 0, s, p); break;
@@ -585,7 +594,7 @@ int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
 // eight and 24 units spills registers: three, twelve and 16 instead); at most 24, more waves beyond.
 template <int KIND>
 int glu_units_a_wave(int64_t units) {
-  const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * kGluWaves;
+  const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * (glu_threads<KIND>() / 64);
   const int64_t need = (units + capacity - 1) / capacity;
   static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 16, 24};
   for (int f : kForms) {
@@ -599,12 +608,13 @@ template <int KIND, int MODE>
 int launch_glu_mode(GluParams& p, hipStream_t s) {
   const int64_t units = (int64_t)p.na * p.nb;
   const int upw = glu_units_a_wave<KIND>(units);
-  const int64_t waves = ((units + upw - 1) / upw + kGluWaves - 1) / kGluWaves * kGluWaves;
+  constexpr int kWaves = glu_threads<KIND>() / 64;
+  const int64_t waves = ((units + upw - 1) / upw + kWaves - 1) / kWaves * kWaves;
   if (waves > INT32_MAX) return STRATA_ERR_SHAPE;
   p.waves = (int)waves;
   p.wave_a = p.waves / p.nb;
   p.wave_b = p.waves % p.nb;
-  return launch_glu_upw<KIND, MODE>(p, upw, dim3((unsigned)(waves / kGluWaves)), s);
+  return launch_glu_upw<KIND, MODE>(p, upw, dim3((unsigned)(waves / kWaves)), s);
 }
 
 template <int KIND>
@@ -648,7 +658,7 @@ bool routed_one32_takes(const MatvecParams& p) {
 
 template <int KIND, bool F32 = false>
 int launch_routed_one(const MatvecParams& mp, hipStream_t s) {
-  if constexpr (KIND != K_Q4_K) {
+  if constexpr ((KIND != K_Q4_K && KIND != K_Q6_K && KIND != K_Q8_0) || (F32 && KIND != K_Q4_K)) {
     return STRATA_ERR_SHAPE;
   } else {
     GluParams p = {};
