@@ -583,6 +583,7 @@ int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
     case 6: hipLaunchKernelGGL((routed_glu_kernel<KIND, 6, MODE>), grid, block, 0, s, p); break;
     case 8: hipLaunchKernelGGL((routed_glu_kernel<KIND, 8, MODE>), grid, block, 0, s, p); break;
     case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MODE>), grid, block, 0, s, p); break;
+    case 15: hipLaunchKernelGGL((routed_glu_kernel<KIND, 15, MODE>), grid, block, 0, s, p); break;
     case 16: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MODE>), grid, block, 0, s, p); break;
     default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 24, MODE>), grid, block, 0, s, p); break;
   }
@@ -591,14 +592,14 @@ int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
 }
 
 // Units a wave: the fewest of the forms built that fit the units into one round of resident waves (IQ3_S at two,
-// eight and 24 units spills registers: three, twelve and 16 instead); at most 24, more waves beyond.
+// eight, 15 and 24 units spills registers: three, twelve and 16 instead); at most 24, more waves beyond.
 template <int KIND>
 int glu_units_a_wave(int64_t units) {
   const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * (glu_threads<KIND>() / 64);
   const int64_t need = (units + capacity - 1) / capacity;
-  static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 16, 24};
+  static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 15, 16, 24};  // 15: five tokens' 40 pairs on every CU
   for (int f : kForms) {
-    if (KIND == K_IQ3_S && (f == 2 || f == 8 || f == 24)) continue;
+    if (KIND == K_IQ3_S && (f == 2 || f == 8 || f == 15 || f == 24)) continue;
     if (f >= need) return f;
   }
   return KIND == K_IQ3_S ? 16 : 24;
