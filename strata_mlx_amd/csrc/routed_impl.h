@@ -541,9 +541,14 @@ int launch_routed_down(const MatvecParams& mp, hipStream_t s) {
     p.pairs = mp.pairs;
     p.share = mp.share;
     const int units_per_pair = (mp.rows + 7) / 8;
-    const int64_t units = (int64_t)units_per_pair * mp.pairs;
-    const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * kGluWaves;
-    const bool two = units > capacity;  // more units than one round of waves: two a wave
+    // units a wave, one or two: the fewer rounds of workgroups (a pair's own) times units a wave (40 pairs of
+    // 4096 rows: 1280 workgroups of one unit a wave, five full rounds, against 640 of two, two and a half)
+    const int64_t cus = (int64_t)device_cus() * kGluGroupsPerCU;
+    auto cost = [&](int upw) {
+      const int64_t groups = (int64_t)((units_per_pair + kGluWaves * upw - 1) / (kGluWaves * upw)) * mp.pairs;
+      return (groups + cus - 1) / cus * upw;
+    };
+    const bool two = cost(2) < cost(1);
     if (mp.cols == 1536)
       return two ? launch_down_su<KIND, 3, 2>(p, units_per_pair, s) : launch_down_su<KIND, 3, 1>(p, units_per_pair, s);
     return two ? launch_down_su<KIND, 5, 2>(p, units_per_pair, s) : launch_down_su<KIND, 5, 1>(p, units_per_pair, s);
