@@ -254,8 +254,12 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
   constexpr int kMaxBuffers = MODE == ONE32 ? 1 : R::kBuffers;  // ONE32 holds two parts of the token
   constexpr int kBuffers = UPW < kMaxBuffers ? UPW : kMaxBuffers;  // units whose rows are in registers at once
   constexpr int kTokens = MODE == GLUN ? kGluMaxTokens : MODE == ONE32 ? 2 : 1;
-  __shared__ u32x2 tab[R::kEntries];
-  __shared__ u32x4 xs[512 * kTokens];
+  // one block of LDS, the table first: its entries then sit below 64 KB, where a lookup's address is the entry's
+  // offset alone (placed after eight tokens' 64 KB, every lookup took an add)
+  __shared__ __attribute__((aligned(16))) uint8_t lds[8 * R::kEntries + 16 * 512 * kTokens + 4 * kGluWaves];
+  u32x2* const tab = reinterpret_cast<u32x2*>(lds);
+  u32x4* const xs = reinterpret_cast<u32x4*>(lds + 8 * R::kEntries);
+  uint32_t* const wmax = reinterpret_cast<uint32_t*>(lds + 8 * R::kEntries + 16 * 512 * kTokens);
   const int tid = threadIdx.x, lane = tid & 63;
   const int gw = blockIdx.x * kGluWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -267,7 +271,6 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
 #pragma unroll
   for (int k = 0; k < kPieceLoads; ++k)
     xpiece[k] = p.x[MODE == ONE32 ? tid : min(tid + k * kGluThreads, 512 * p.tokens - 1)];
-  __shared__ uint32_t wmax[kGluWaves];
 
   // the wave's units (pair, row) and whether each is live; ONE: row is the unit's first row (2 i), pair 0
   int pair[UPW], row[UPW];
