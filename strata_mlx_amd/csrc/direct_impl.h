@@ -257,6 +257,18 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t b, uint32_t* w2) {
   w2[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) - k);
 }
 
+// Four code bytes -> two words of float16 1024 + code (exact), the bias left to the sum: 1024 + code times x
+// summed is the codes' sum plus 1024 times the sum of x, which apply_run takes off once a run (or half run), not
+// once a weight pair.
+__device__ __forceinline__ void bytes_to_h2_biased(uint32_t b, uint32_t* w2) {
+  w2[0] = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+  w2[1] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+}
+// The kinds whose decode_run leaves that bias in: the sum of x it needs (x_sums) is the lane's, the same for
+// every row, so the matvecs compute it once a token.
+template <int KIND>
+constexpr bool kBiasedRuns = KIND == K_Q4_K || KIND == K_Q5_K || KIND == K_Q6_K;
+
 // A run's scales: a (every kind), b (Q4_K: dmin * min, subtracted times the run's sum of x; Q6_K: the second
 // 16 weights' scale, a the first 16's).
 struct RunScale {
@@ -298,7 +310,7 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
     for (int i = 0; i < 8; ++i) {
       uint32_t c = (f.qs[i / 4][i % 4] >> (4 * h)) & 0x0F0F0F0Fu;
       if constexpr (KIND == K_Q5_K) c |= ((f.qh[i / 4][i % 4] >> sb) & 0x01010101u) << 4;
-      bytes_to_h2<0>(c, w + 2 * i);
+      bytes_to_h2_biased(c, w + 2 * i);  // 1024 + code
     }
     // its 6-bit scale and min from the 12 packed bytes p
     const uint32_t b0 = (f.sm[0] >> tb) & 255, b1 = (f.sm[1] >> tb) & 255, b2 = (f.sm[2] >> tb) & 255;
@@ -312,7 +324,7 @@ __device__ __forceinline__ RunScale decode_run(const RunPair<KIND>& f, int h, in
     for (int i = 0; i < 8; ++i) {
       const uint32_t lo = (f.ql[i / 4][i % 4] >> (4 * h)) & 0x0F0F0F0Fu;
       const uint32_t hb = (f.qh[i / 4][i % 4] >> r2) & 0x03030303u;
-      bytes_to_h2<32>(lo | (hb << 4), w + 2 * i);
+      bytes_to_h2_biased(lo | (hb << 4), w + 2 * i);  // 1024 + code: 1056 + the weight's (code - 32)
     }
     const float d = half_bits(f.d);
     return RunScale{d * (float)(int8_t)(f.sc[h] & 255), d * (float)(int8_t)(f.sc[h] >> 8)};
@@ -377,19 +389,42 @@ __device__ __forceinline__ float dot_n(const uint32_t* w, const uint32_t* x) {
   return a + b;
 }
 
-// The run's sum against 32 activations (16 packed pairs).
+// The sums of x a biased run needs (kBiasedRuns): Q4_K, Q5_K the run's 32 activations; Q6_K each half's 16.
 template <int KIND>
-__device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w, const uint32_t* x) {
-  if constexpr (KIND == K_Q4_K || KIND == K_Q5_K) {
-    const uint32_t ones[16] = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
-                               0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
-                               0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
-    return s.a * dot16x2(w, x) - s.b * dot_n<16>(ones, x);
-  } else if constexpr (KIND == K_Q6_K || KIND == K_Q3_K) {  // a scale every 16 weights
+__device__ __forceinline__ void x_sums(const uint32_t* x, float* xs) {
+  const uint32_t ones[16] = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                             0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                             0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+  if constexpr (KIND == K_Q6_K) {
+    xs[0] = dot_n<8>(ones, x);
+    xs[1] = dot_n<8>(ones, x + 8);
+  } else if constexpr (KIND == K_Q4_K || KIND == K_Q5_K) {
+    xs[0] = dot_n<16>(ones, x);
+  }
+}
+// per run h of a lane's run pair: the floats of x_sums at xs + kXSums * h
+template <int KIND>
+constexpr int kXSums = KIND == K_Q6_K ? 2 : kBiasedRuns<KIND> ? 1 : 0;
+
+// The run's sum against 32 activations (16 packed pairs); xs: the run's sums of x (x_sums) for a biased run.
+template <int KIND>
+__device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w, const uint32_t* x, const float* xs) {
+  if constexpr (KIND == K_Q4_K || KIND == K_Q5_K) {  // a (code . x) - b sum x, the codes 1024 too high
+    return s.a * dot16x2(w, x) - (s.b + 1024.0f * s.a) * xs[0];
+  } else if constexpr (KIND == K_Q6_K) {  // a scale every 16 weights, the weights 1056 too high
+    return s.a * (dot_n<8>(w, x) - 1056.0f * xs[0]) + s.b * (dot_n<8>(w + 8, x + 8) - 1056.0f * xs[1]);
+  } else if constexpr (KIND == K_Q3_K) {  // a scale every 16 weights
     return s.a * dot_n<8>(w, x) + s.b * dot_n<8>(w + 8, x + 8);
   } else {
     return s.a * dot16x2(w, x);
   }
+}
+// the same with the sums of x taken here
+template <int KIND>
+__device__ __forceinline__ float apply_run(const RunScale& s, const uint32_t* w, const uint32_t* x) {
+  float xs[2] = {0.0f, 0.0f};
+  if constexpr (kBiasedRuns<KIND>) x_sums<KIND>(x, xs);
+  return apply_run<KIND>(s, w, x, xs);
 }
 
 // float16 bits of a non-negative integer below 2048 (exact): the codebooks' float16 entries, at compile time.
@@ -964,6 +999,16 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
         arrived(x[t]);
       }
     }
+    float xsum[TT][2 * kXSums<KIND> + 1];  // the tokens' sums of x for biased runs, once a pass
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if constexpr (kBiasedRuns<KIND>) {
+        if (t < nq) {
+          x_sums<KIND>(x[t], xsum[t]);
+          x_sums<KIND>(x[t] + 16, xsum[t] + kXSums<KIND>);
+        }
+      }
+    }
     float acc[TT][RU];
     float sums[RU][TT];  // row sums of the run-time reduction
 #pragma unroll
@@ -978,7 +1023,7 @@ __global__ __launch_bounds__(kThreads, TT == 1 ? 4 : 3) void direct_decode_kerne
         const RunScale rs = decode_run<KIND>(f[s], h, jp, w, tab);
 #pragma unroll
         for (int t = 0; t < TT; ++t)
-          if (t < nq) acc[t][s] += apply_run<KIND>(rs, w, x[t] + 16 * h);
+          if (t < nq) acc[t][s] += apply_run<KIND>(rs, w, x[t] + 16 * h, xsum[t] + kXSums<KIND> * h);
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {

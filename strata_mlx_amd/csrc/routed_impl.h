@@ -61,27 +61,30 @@ struct Routed {
   static __device__ __forceinline__ void load(const uint8_t* row, int j, Fields& f) {
     load_fields<KIND>(row, 0u, lane_offsets<KIND>(j), f);
   }
-  static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const u32x2* tab) {
+  // xs: the lane's sums of x for biased runs (x_sums of both runs, kXSums a run), the same for every unit
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const float* xs,
+                                                   const u32x2* tab) {
     const DirectTables<KIND>& t = *reinterpret_cast<const DirectTables<KIND>*>(tab);  // unused by these types
     float s = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t w[16];
       const RunScale rs = decode_run<KIND>(f, h, j, w, t);
-      s += apply_run<KIND>(rs, w, x + 16 * h);
+      s += apply_run<KIND>(rs, w, x + 16 * h, xs + kXSums<KIND> * h);
     }
     return s;
   }
   // the same against x_a + x_b (a float32 token as two float16 parts): each run decoded once
   static __device__ __forceinline__ float pair_sum2(const Fields& f, int j, const uint32_t* xa, const uint32_t* xb,
-                                                    const u32x2* tab) {
+                                                    const float* xsa, const float* xsb, const u32x2* tab) {
     const DirectTables<KIND>& t = *reinterpret_cast<const DirectTables<KIND>*>(tab);
     float s = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t w[16];
       const RunScale rs = decode_run<KIND>(f, h, j, w, t);
-      s += apply_run<KIND>(rs, w, xa + 16 * h) + apply_run<KIND>(rs, w, xb + 16 * h);
+      s += apply_run<KIND>(rs, w, xa + 16 * h, xsa + kXSums<KIND> * h) +
+           apply_run<KIND>(rs, w, xb + 16 * h, xsb + kXSums<KIND> * h);
     }
     return s;
   }
@@ -144,7 +147,8 @@ struct Routed<K_IQ3_S> {
     return dot16x2(w, x + 16 * h);
   }
   // lane j's share of a row: its two runs, each times its scale d (1 + 2 s)
-  static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const u32x2* tab) {
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const float*,
+                                                   const u32x2* tab) {
     const float d = half_bits(f.d);
     const uint32_t sc = (uint32_t)f.sc >> (8 * (j & 1));
     const float s0 = d * (float)(1 + 2 * (sc & 15u)), s1 = d * (float)(1 + 2 * ((sc >> 4) & 15u));
@@ -187,7 +191,8 @@ struct Routed<K_Q2_0> {
     }
     return dot16x2(w, x + 16 * h);
   }
-  static __device__ __forceinline__ float pair_sum(const Fields& f, int, const uint32_t* x, const u32x2* tab) {
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int, const uint32_t* x, const float*,
+                                                   const u32x2* tab) {
     return half_bits(f.d) * (run(f, 0, x, tab) + run(f, 1, x, tab));
   }
 };
@@ -223,16 +228,17 @@ __device__ __forceinline__ int x_piece_slot(int c) { return glu_x_slot(c >> 3, c
 // wave: the first row's total and the second's, the same in every lane (read into scalars).
 template <int KIND, bool TWO = false>
 __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], int lane, const uint32_t* x,
-                                         const uint32_t* x2, const u32x2* tab, float& gate, float& up) {
+                                         const uint32_t* x2, const float* xs, const float* xs2, const u32x2* tab,
+                                         float& gate, float& up) {
   opaque(f[0]);  // nothing of the decode is done before the workgroup barrier (it would wait for these rows there)
   opaque(f[1]);
   float g, u;
   if constexpr (TWO) {
-    g = Routed<KIND>::pair_sum2(f[0], lane, x, x2, tab);
-    u = Routed<KIND>::pair_sum2(f[1], lane, x, x2, tab);
+    g = Routed<KIND>::pair_sum2(f[0], lane, x, x2, xs, xs2, tab);
+    u = Routed<KIND>::pair_sum2(f[1], lane, x, x2, xs, xs2, tab);
   } else {
-    g = Routed<KIND>::pair_sum(f[0], lane, x, tab);
-    u = Routed<KIND>::pair_sum(f[1], lane, x, tab);
+    g = Routed<KIND>::pair_sum(f[0], lane, x, xs, tab);
+    u = Routed<KIND>::pair_sum(f[1], lane, x, xs, tab);
   }
   // lanes 0-31 the first row's partial sums two at a time, lanes 32-63 the second's; then within the halves
   float v = sum_swapped(g, u, 32);
@@ -255,11 +261,13 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
   constexpr int kBuffers = UPW < kMaxBuffers ? UPW : kMaxBuffers;  // units whose rows are in registers at once
   constexpr int kTokens = MODE == GLUN ? kGluMaxTokens : MODE == ONE32 ? 2 : 1;
   // one block of LDS, the table first: its entries then sit below 64 KB, where a lookup's address is the entry's
-  // offset alone (placed after eight tokens' 64 KB, every lookup took an add)
-  __shared__ __attribute__((aligned(16))) uint8_t lds[8 * R::kEntries + 16 * 512 * kTokens + 4 * kGluWaves];
+  // offset alone (placed after eight tokens' 64 KB, every lookup took an add); the tokens at a multiple of 16
+  // bytes (a 16-byte LDS read at any other address runs many times slower)
+  constexpr int kTabBytes = (8 * R::kEntries + 15) / 16 * 16;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kTabBytes + 16 * 512 * kTokens + 4 * kGluWaves];
   u32x2* const tab = reinterpret_cast<u32x2*>(lds);
-  u32x4* const xs = reinterpret_cast<u32x4*>(lds + 8 * R::kEntries);
-  uint32_t* const wmax = reinterpret_cast<uint32_t*>(lds + 8 * R::kEntries + 16 * 512 * kTokens);
+  u32x4* const xs = reinterpret_cast<u32x4*>(lds + kTabBytes);
+  uint32_t* const wmax = reinterpret_cast<uint32_t*>(lds + kTabBytes + 16 * 512 * kTokens);
   const int tid = threadIdx.x, lane = tid & 63;
   const int gw = blockIdx.x * kGluWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -380,6 +388,18 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
   Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
+  // the lane's sums of x for biased runs (the linear types: one token here), once for every unit, after the rows
+  // are asked for (taken before, they held the loads back until the token's LDS reads were in)
+  static_assert(!(kBiasedRuns<KIND> && MODE == GLUN), "the linear types at one token");
+  float xsum[2 * kXSums<KIND> + 1], xsum2[2 * kXSums<KIND> + 1];
+  if constexpr (kBiasedRuns<KIND> && MODE != GLUN) {
+    x_sums<KIND>(x, xsum);
+    x_sums<KIND>(x + 16, xsum + kXSums<KIND>);
+    if constexpr (MODE == ONE32) {
+      x_sums<KIND>(x2, xsum2);
+      x_sums<KIND>(x2 + 16, xsum2 + kXSums<KIND>);
+    }
+  }
 
   // lane k collects unit k's two totals
   float gv = 0.0f, uv = 0.0f;
@@ -389,7 +409,7 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
       if (k == 0 || pair[k] != pair[k - 1]) read_x(pair[k] / p.share, x);
     }
     float g, u;
-    glu_unit<KIND, MODE == ONE32>(f[k % kBuffers], lane, x, x2, tab, g, u);
+    glu_unit<KIND, MODE == ONE32>(f[k % kBuffers], lane, x, x2, xsum, xsum2, tab, g, u);
     if (k + kBuffers < UPW) issue(k + kBuffers, f[k % kBuffers]);
     gv = lane == k ? g : gv;
     uv = lane == k ? u : uv;
@@ -495,7 +515,12 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams 
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
       }
-      acc += R::pair_sum(f[k][st], j, x, tab);
+      float xsum[2 * kXSums<KIND> + 1];
+      if constexpr (kBiasedRuns<KIND>) {
+        x_sums<KIND>(x, xsum);
+        x_sums<KIND>(x + 16, xsum + kXSums<KIND>);
+      }
+      acc += R::pair_sum(f[k][st], j, x, xsum, tab);
     }
     acc += lanes_apart(acc, 1);
     acc += lanes_apart(acc, 2);
