@@ -62,6 +62,17 @@ struct Routed {
     load_fields<KIND>(row, 0u, lane_offsets<KIND>(j), f);
   }
   // xs: the lane's sums of x for biased runs (x_sums of both runs, kXSums a run), the same for every unit
+  static constexpr int kPrepSums = 2 * kXSums<KIND>;  // xs: the sums of x of both runs (x_sums)
+  static __device__ __forceinline__ void prep_x(uint32_t* x, float* xs) {
+    if constexpr (kBiasedRuns<KIND>) {
+      x_sums<KIND>(x, xs);
+      x_sums<KIND>(x + 16, xs + kXSums<KIND>);
+    }
+  }
+  static __device__ __forceinline__ float pair_sum_lds(const Fields& f, int j, const uint32_t* x, const float* xs,
+                                                       const u32x2* tab) {
+    return pair_sum(f, j, x, xs, tab);
+  }
   static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const float* xs,
                                                    const u32x2* tab) {
     const DirectTables<KIND>& t = *reinterpret_cast<const DirectTables<KIND>*>(tab);  // unused by these types
@@ -147,6 +158,12 @@ struct Routed<K_IQ3_S> {
     return dot16x2(w, x + 16 * h);
   }
   // lane j's share of a row: its two runs, each times its scale d (1 + 2 s)
+  static constexpr int kPrepSums = 0;
+  static __device__ __forceinline__ void prep_x(uint32_t*, float*) {}
+  static __device__ __forceinline__ float pair_sum_lds(const Fields& f, int j, const uint32_t* x, const float* xs,
+                                                       const u32x2* tab) {
+    return pair_sum(f, j, x, xs, tab);
+  }
   static __device__ __forceinline__ float pair_sum(const Fields& f, int j, const uint32_t* x, const float*,
                                                    const u32x2* tab) {
     const float d = half_bits(f.d);
@@ -191,9 +208,56 @@ struct Routed<K_Q2_0> {
     }
     return dot16x2(w, x + 16 * h);
   }
-  static __device__ __forceinline__ float pair_sum(const Fields& f, int, const uint32_t* x, const float*,
-                                                   const u32x2* tab) {
+  // down (routed_down_kernel): the table
+  static __device__ __forceinline__ float pair_sum_lds(const Fields& f, int, const uint32_t* x, const float*,
+                                                       const u32x2* tab) {
     return half_bits(f.d) * (run(f, 0, x, tab) + run(f, 1, x, tab));
+  }
+  // Gate and up (routed_glu_kernel) decode in registers, no table: byte b of a run (codes c0..c3 of weights
+  // 4b .. 4b + 3) goes to bytes 0 and 2 of a word (one v_perm), and two and-ors with 0x6400 give the float16
+  // integers 1024 + c0, 1024 + 4 c1 and 1024 + 16 c2, 1024 + 64 c3 (exact). The token was divided weight by
+  // weight by 1, 4, 16, 64 (prep_x: exact powers of two), so each product is 1024 x' + c x, and the run's
+  // 1024 sum x' + sum x (in xs) takes off the 1024 and the 1 of c - 1. A lookup table's 8-byte reads at random
+  // entries left half the LDS cycles to bank conflicts.
+  static constexpr int kPrepSums = 2;  // xs: one float a run
+  static __device__ __forceinline__ void prep_x(uint32_t* x, float* xs) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const uint32_t ones[16] = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                               0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u,
+                               0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float sx = dot_n<16>(ones, x + 16 * h);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const h2v m = (i & 1) ? h2v{(_Float16)0.0625f, (_Float16)0.015625f} : h2v{(_Float16)1.0f, (_Float16)0.25f};
+        x[16 * h + i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, x[16 * h + i]) * m);
+      }
+      xs[h] = 1024.0f * dot_n<16>(ones, x + 16 * h) + sx;
+    }
+  }
+  static __device__ __forceinline__ float pair_sum(const Fields& f, int, const uint32_t* x, const float* xs,
+                                                   const u32x2*) {
+    // the masks and 0x6400 0x6400 in registers: an and-or takes three, and a VALU instruction of three operands
+    // here takes no literal and one scalar register at most
+    uint32_t m01, m23, base;
+    asm("v_mov_b32 %0, 0x000C0003" : "=v"(m01));
+    asm("v_mov_b32 %0, 0x00C00030" : "=v"(m23));
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(base));
+    float s = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w[16];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const uint32_t q = f.qs[2 * h + (l >> 2)], k = (uint32_t)(l & 3);
+        const uint32_t dup = __builtin_amdgcn_perm(q, q, 0x0C000C00u | (k << 16) | k);  // byte k at bytes 0, 2
+        w[2 * l] = (dup & m01) | base;
+        w[2 * l + 1] = (dup & m23) | base;
+      }
+      s += dot16x2(w, x + 16 * h) - xs[h];
+    }
+    return half_bits(f.d) * s;
   }
 };
 
@@ -388,25 +452,22 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
   Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
-  // the lane's sums of x for biased runs (the linear types: one token here), once for every unit, after the rows
-  // are asked for (taken before, they held the loads back until the token's LDS reads were in)
-  static_assert(!(kBiasedRuns<KIND> && MODE == GLUN), "the linear types at one token");
-  float xsum[2 * kXSums<KIND> + 1], xsum2[2 * kXSums<KIND> + 1];
-  if constexpr (kBiasedRuns<KIND> && MODE != GLUN) {
-    x_sums<KIND>(x, xsum);
-    x_sums<KIND>(x + 16, xsum + kXSums<KIND>);
-    if constexpr (MODE == ONE32) {
-      x_sums<KIND>(x2, xsum2);
-      x_sums<KIND>(x2 + 16, xsum2 + kXSums<KIND>);
-    }
-  }
+  // what the type takes from the token once for every unit (the linear types' sums of x, Q2_0's scaled token and
+  // its sums), after the rows are asked for (taken before, they held the loads back until the token's LDS reads
+  // were in); GLUN: at each new pair, below
+  float xsum[R::kPrepSums + 1], xsum2[R::kPrepSums + 1];
+  if constexpr (MODE != GLUN) R::prep_x(x, xsum);
+  if constexpr (MODE == ONE32) R::prep_x(x2, xsum2);
 
   // lane k collects unit k's two totals
   float gv = 0.0f, uv = 0.0f;
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
     if constexpr (MODE == GLUN) {
-      if (k == 0 || pair[k] != pair[k - 1]) read_x(pair[k] / p.share, x);
+      if (k == 0 || pair[k] != pair[k - 1]) {
+        read_x(pair[k] / p.share, x);
+        R::prep_x(x, xsum);
+      }
     }
     float g, u;
     glu_unit<KIND, MODE == ONE32>(f[k % kBuffers], lane, x, x2, xsum, xsum2, tab, g, u);
@@ -520,7 +581,7 @@ __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams 
         x_sums<KIND>(x, xsum);
         x_sums<KIND>(x + 16, xsum + kXSums<KIND>);
       }
-      acc += R::pair_sum(f[k][st], j, x, xsum, tab);
+      acc += R::pair_sum_lds(f[k][st], j, x, xsum, tab);
     }
     acc += lanes_apart(acc, 1);
     acc += lanes_apart(acc, 2);
