@@ -16,7 +16,8 @@ Beside it, on the same line, the other workloads of the path:
   dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K fused into one launch, o
                  Q8_0, the shared expert's Q4_K gate and up 1536 x 4096 with the SwiGLU in one launch and its
                  down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16 token each (graphs over copies, at least
-                 1 GB a graph)
+                 1 GB a graph); shared_in_routed: the shared expert's gate and up taken by the headline layers'
+                 routed gate+up launches instead (its marginal time over those launches alone)
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
                  the dense layers as tile products, TFLOPS
   roofline       the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
@@ -208,6 +209,57 @@ def dense_bench(B, synth, dev, steps, warmup):
             "unit": "GB/s", "us_per_token": round(total_s * 1e6, 1), "bytes_per_token": total_bytes,
             "hbm_frac": round(total_bytes / total_s / 1e9 / HBM_PEAK_GBS, 4), "dtype": "f16",
             "data": "synthetic (random blocks)", "layers": out}
+
+
+def shared_fused_bench(B, D, synth, dev, lins, steps, warmup, rng):
+    """One decode token's routed gate/up/SwiGLU (the layers' IQ3_S stacks, 256 experts top-8) with a shared expert's
+    Q4_K gate and up (1536 x 4096 each) in the same launch (blocks.gate_up_swiglu_shared), against the routed launch
+    alone and the two launches apart: the shared expert's marginal time a layer and its bytes' rate over it."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    routes = [synth.zipf_routing(1, E, K, rng)[0] for _ in lins]
+    idx = [torch.from_numpy(r).to(torch.int32).to(dev).reshape(-1) for r in routes]
+    x = (torch.randn((1, H), device=dev) / 8).half()
+    shared = [tuple(D.BlockLinear(synth.random_stack("Q4_K", F * H, dev, g), "Q4_K", (F, H)) for _ in range(2))
+              for _ in lins]
+
+    def alone():
+        for (gate, up, _), ix in zip(lins, idx):
+            B.gate_up_swiglu(gate, up, x, ix, K)
+
+    def apart():
+        for (gate, up, _), ix, (sg, su) in zip(lins, idx, shared):
+            B.gate_up_swiglu(gate, up, x, ix, K)
+            D.gate_up_swiglu(sg, su, x)
+
+    def fused():
+        for (gate, up, _), ix, (sg, su) in zip(lins, idx, shared):
+            if B.gate_up_swiglu_shared(gate, up, x, ix, sg, su) is None:
+                raise RuntimeError("the routed launch did not take the shared expert")
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):  # one eager pass of each first: the library's lazy state, torch's allocator
+        for run in (alone, apart, fused):
+            run()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graphs = {}
+    for name, run in (("alone", alone), ("apart", apart), ("fused", fused)):
+        graphs[name] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[name]):
+            run()
+    us = {name: time_graph(gr, steps, warmup) / steps / len(lins) * 1e6 for name, gr in graphs.items()}
+    mat_bytes = lins[0][0].blocks.numel() // E
+    routed_bytes = sum(len(np.unique(r)) * 2 * mat_bytes for r in routes) / len(lins) + H * 2 + K * F * 2
+    shared_bytes = 2 * shared[0][0].blocks.numel() + F * 2  # gate and up in, h out (x counted with the routed)
+    marginal = us["fused"] - us["alone"]
+    return {"workload": f"one decode token's gate/up/SwiGLU, {len(lins)} layers: routed IQ3_S 256 experts top-8 + "
+                        f"shared expert Q4_K {F} x {H} gate and up",
+            "routed_us": round(us["alone"], 3), "apart_us": round(us["apart"], 3), "fused_us": round(us["fused"], 3),
+            "shared_bytes": int(shared_bytes), "shared_marginal_us": round(marginal, 3),
+            "shared_hbm_frac": round(shared_bytes / (marginal * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if marginal > 0 else None,
+            "fused_hbm_frac": round((routed_bytes + shared_bytes) / (us["fused"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def host_cpu():
@@ -418,8 +470,11 @@ def main():
         dd = dense_bench(B, synth, dev, max(2, args.steps // 5), 2)
         result["dense_decode"] = {k: dd[k] for k in ("value", "unit", "us_per_token", "bytes_per_token", "hbm_frac")}
         result["dense_decode"]["layers"] = {n: {k: v[k] for k in ("kind", "us", "hbm_frac")} for n, v in dd["layers"].items()}
-        note("2048-token prefill")
         from strata_mlx_amd import dense as D
+        note("shared expert's gate and up in the routed launch")
+        result["dense_decode"]["shared_in_routed"] = shared_fused_bench(B, D, synth, dev, lins, args.steps, args.warmup,
+                                                                        rng)
+        note("2048-token prefill")
         result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng)
     if not args.no_cpu_baseline:
         note("cpu baseline")

@@ -72,6 +72,19 @@ int strata_expert_gate_up_swiglu(int kind, const void* gate_blocks, const void* 
                                  int x_dtype, int64_t share, void* out_gate, void* out_up, void* out_h,
                                  void* stream);
 
+/* strata_expert_gate_up_swiglu at one token (every pair reads x's one row) with a shared expert's gate and up
+ * in the same launch: shared_h[r] = silu(shared_gate[r, :] . x) * (shared_up[r, :] . x), rounded as out_h;
+ * shared_gate, shared_up (shared_rows, cols). The routed stacks IQ3_S or Q2_0 of 4096 inputs, x float16, the
+ * shared expert Q4_K; other cases return STRATA_ERR_SHAPE, and the caller makes the two calls apart. No single
+ * counterpart in the reference, whose MoE block calls the routed experts and then the shared expert
+ * (strata_mlx/fused.py:492-493, the gate and up of each, with the SwiGLU of their down calls): the routed
+ * launch's waves take the shared expert's rows among their own, which spares its own launch. */
+int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts,
+                                        int64_t rows, int64_t cols, const uint32_t* idx, int64_t pairs,
+                                        const void* x, int x_dtype, void* out_gate, void* out_up, void* out_h,
+                                        int shared_kind, const void* shared_gate, const void* shared_up,
+                                        int64_t shared_rows, void* shared_h, void* stream);
+
 /* out[p, r] = W[idx[p], r, :] . swiglu(gate[p], up[p]) with the SwiGLU rounded as mlx-lm rounds it
  * (sigmoid in float32 rounded to the activation dtype, then two products in that dtype); gate, up
  * (pairs, cols). Replaces matvec_glu + _MATVEC_GLU, strata_mlx/blocks.py:939-955, 225-259. */

@@ -143,6 +143,41 @@ def gate_up_swiglu(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tens
     return g, u, h
 
 
+def gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tensor, idx: torch.Tensor,
+                          shared_gate, shared_up):
+    """gate_up_swiglu at one token with a shared expert's gate and up (layers of the file's Q4_K blocks with
+    `blocks`, `kind`, `output_dims`, `input_dims`: dense.BlockLinear) in the same launch: (g, u, h) of the pairs
+    and the shared expert's h (1, shared rows). None where the launch does not take the case (other types, several
+    tokens, inputs other than 4096): the caller then makes the two calls apart. The routed experts' and the shared
+    expert's gate and up of strata_mlx/fused.py:492-493, with the SwiGLU of their down calls."""
+    if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) != (up.kind, up.output_dims, up.input_dims,
+                                                                             up.num_experts):
+        raise ValueError("gate and up differ in type or shape")
+    if (shared_gate.kind, shared_gate.output_dims, shared_gate.input_dims) != (
+            shared_up.kind, shared_up.output_dims, shared_up.input_dims) or shared_gate.input_dims != gate.input_dims:
+        raise ValueError("the shared expert's gate and up differ in type or shape from each other or the token")
+    if getattr(shared_gate, "blocks", None) is None or getattr(shared_up, "blocks", None) is None or \
+            getattr(shared_gate, "to_file", None) is not None or getattr(shared_up, "to_file", None) is not None:
+        raise ValueError("the shared expert's layers as the file's blocks, inputs in the file's order")
+    pairs = idx.numel()
+    x2 = x.reshape(-1, gate.input_dims).contiguous()
+    if x2.shape[0] != 1:
+        return None
+    g = torch.empty((pairs, gate.output_dims), dtype=x.dtype, device=x.device)
+    u, h = torch.empty_like(g), torch.empty_like(g)
+    sh = torch.empty((1, shared_gate.output_dims), dtype=x.dtype, device=x.device)
+    idx = _idx32(idx)
+    rc = _lib.library().strata_expert_gate_up_swiglu_shared(
+        _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), gate.num_experts, gate.output_dims,
+        gate.input_dims, idx.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), g.data_ptr(), u.data_ptr(),
+        h.data_ptr(), _lib.kind_id(shared_gate.kind), shared_gate.blocks.data_ptr(), shared_up.blocks.data_ptr(),
+        shared_gate.output_dims, sh.data_ptr(), _lib.stream())
+    if rc in (_lib.ERR_SHAPE, _lib.ERR_DTYPE):
+        return None
+    _lib.check(rc, f"gate/up/swiglu with the shared expert {gate.kind} + {shared_gate.kind}")
+    return g, u, h, sh
+
+
 def expert_matvec(lin: BlockSwitchLinear, idx: torch.Tensor, x: torch.Tensor, share: int = 1) -> torch.Tensor:
     """out[pair] = W[idx[pair]] . x[pair / share]: x (pairs / share, in) -> (pairs, out)."""
     pairs = idx.numel()

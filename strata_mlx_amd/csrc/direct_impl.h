@@ -1351,6 +1351,12 @@ namespace strata_mv {
 // direct kernel, else the persistent wave kernel, else the staged fast kernel; other cases the generic kernels.
 template <int KIND>
 int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int grid_y, int grid_z, hipStream_t s) {
+  // a shared expert in the routed launch: only the persistent routed forms take it
+  if (p.shared[0] != nullptr) {
+    if (!glu && x_dtype == DT_F16 && out_dtype == DT_F16 && grid_z == 2 && routed_glu_takes<KIND>(p))
+      return launch_routed_glu<KIND>(p, s);
+    return STRATA_ERR_SHAPE;
+  }
   // a float32 token against Q4_K rows of 4096 inputs: the persistent form, the token in two float16 parts
   if (!glu && x_dtype == DT_F32 && out_dtype == DT_F32 && routed_one32_takes<KIND>(p))
     return launch_routed_one<KIND, true>(p, s);

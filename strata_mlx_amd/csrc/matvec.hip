@@ -188,6 +188,46 @@ int strata_expert_gate_up_swiglu(int kind, const void* gate_blocks, const void* 
                        out_gate, out_up, false, stream, out_h);
 }
 
+int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts,
+                                        int64_t rows, int64_t cols, const uint32_t* idx, int64_t pairs,
+                                        const void* x, int x_dtype, void* out_gate, void* out_up, void* out_h,
+                                        int shared_kind, const void* shared_gate, const void* shared_up,
+                                        int64_t shared_rows, void* shared_h, void* stream) {
+  MatvecParams p = {};
+  int rc = block_shape(kind, rows, cols, &p.row_bytes);
+  if (rc) return rc;
+  int s_row_bytes = 0;
+  rc = block_shape(shared_kind, shared_rows, cols, &s_row_bytes);
+  if (rc) return rc;
+  if (x_dtype != DT_F16) return STRATA_ERR_DTYPE;
+  if (pairs < 1 || experts < 1 || experts > INT32_MAX || shared_rows < 1) return STRATA_ERR_ARG;
+  if (rows == 0) return STRATA_ERR_SHAPE;  // no routed launch to carry the shared expert: the two calls apart
+  if (!gate_blocks || !up_blocks || !idx || !x || !out_h || !shared_gate || !shared_up || !shared_h)
+    return STRATA_ERR_ARG;
+  if (shared_kind != K_Q4_K || pairs > 65535 || shared_rows > INT32_MAX / 2) return STRATA_ERR_SHAPE;
+  p.blocks[0] = (const uint8_t*)gate_blocks;
+  p.blocks[1] = (const uint8_t*)up_blocks;
+  p.out[0] = out_gate;
+  p.out[1] = out_up;
+  p.glu_out = out_h;
+  p.idx = idx;
+  p.x = x;
+  p.mat_bytes = rows * (int64_t)p.row_bytes;
+  p.experts = experts;
+  p.src_rows = (int)rows;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.pairs = (int)pairs;
+  p.share = (int)pairs;  // one token
+  p.mode = MODE_EXPERT;
+  p.shared[0] = (const uint8_t*)shared_gate;
+  p.shared[1] = (const uint8_t*)shared_up;
+  p.shared_out = shared_h;
+  p.shared_rows = (int)shared_rows;
+  p.shared_row_bytes = s_row_bytes;
+  return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 2, (hipStream_t)stream);
+}
+
 int strata_expert_matvec_swiglu(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
                                 const uint32_t* idx, int64_t pairs, const void* gate, const void* up, int act_dtype,
                                 void* out, void* stream) {

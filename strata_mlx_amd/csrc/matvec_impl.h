@@ -45,6 +45,10 @@ struct MatvecParams {
   int nz, ntiles, items;       // persistent decode: stacks, row tiles per matrix, work items
   int mode;
   int stage_bytes;             // LDS bytes for the staged rows
+  // a shared expert in the routed gate/up launch (one token): its Q4_K gate and up (shared_rows x cols) and its h
+  const uint8_t* shared[2];
+  void* shared_out;
+  int shared_rows, shared_row_bytes;
 };
 
 // Copy [src, src + len) to LDS at dst + (src & 15), 16-byte loads for the aligned middle.

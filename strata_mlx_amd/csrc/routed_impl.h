@@ -280,6 +280,12 @@ struct GluParams {
   // units: u = a * nb + b, (a, b) = (pair, row) for one token, (row, pair) for several; from a wave's unit to its
   // next, (a, b) moves by (wave_a, wave_b) with a carry
   int na, nb, wave_a, wave_b;
+  // the shared expert in the same launch (one token, routed_glu_kernel's SHARED form): its gate and up (Q4_K,
+  // s_rows x 4096) and silu(gate . x) * (up . x) out; its unit r (row r of each) is wave r * waves / s_rows's
+  const uint8_t* s_gate;
+  const uint8_t* s_up;
+  f16* s_h;
+  int s_rows, s_row_bytes;
 };
 
 // A token's piece c (16 bytes: columns 8 c .. 8 c + 7) in LDS: slot c with its low three bits XORed with the
@@ -315,13 +321,14 @@ __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], 
   up = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
-template <int KIND, int UPW, int MODE>
+template <int KIND, int UPW, int MODE, bool SHARED = false>
 __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) void routed_glu_kernel(GluParams p) {
   constexpr int kGluThreads = glu_threads<KIND>(), kGluWaves = kGluThreads / 64;
   typedef Routed<KIND> R;
   typedef typename R::Fields Fields;
   constexpr bool kOne = MODE == ONE || MODE == ONE32;
-  constexpr int kMaxBuffers = MODE == ONE32 ? 1 : R::kBuffers;  // ONE32 holds two parts of the token
+  // units whose rows are in registers at once: ONE32 holds two parts of the token, SHARED the shared expert's unit
+  constexpr int kMaxBuffers = MODE == ONE32 ? 1 : SHARED ? R::kBuffers - 1 : R::kBuffers;
   constexpr int kBuffers = UPW < kMaxBuffers ? UPW : kMaxBuffers;  // units whose rows are in registers at once
   constexpr int kTokens = MODE == GLUN ? kGluMaxTokens : MODE == ONE32 ? 2 : 1;
   // one block of LDS, the table first: its entries then sit below 64 KB, where a lookup's address is the entry's
@@ -452,6 +459,22 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
   Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
+  // the shared expert's unit of this wave (SHARED), if it has one: the first s with s * waves >= gw * s_rows,
+  // if s * waves < (gw + 1) * s_rows; its rows asked for with the routed units' first ones, decoded after them
+  typedef Routed<K_Q4_K> RS;
+  typename RS::Fields fs[2];
+  int s_unit = -1;
+  if constexpr (SHARED) {
+    static_assert(MODE == GLU1, "the shared expert at one token");
+    const int64_t num = (int64_t)gw * p.s_rows;
+    const int64_t su = (num + p.waves - 1) / p.waves;
+    if (su < p.s_rows && su * p.waves < num + p.s_rows) s_unit = (int)su;
+    if (s_unit >= 0) {
+      const int64_t off = (int64_t)s_unit * p.s_row_bytes;
+      RS::load(p.s_gate + off, lane, fs[0]);
+      RS::load(p.s_up + off, lane, fs[1]);
+    }
+  }
   // what the type takes from the token once for every unit (the linear types' sums of x, Q2_0's scaled token and
   // its sums), after the rows are asked for (taken before, they held the loads back until the token's LDS reads
   // were in); GLUN: at each new pair, below
@@ -507,6 +530,21 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
       if (p.out_gate != nullptr) p.out_gate[o] = gq;
       if (p.out_up != nullptr) p.out_up[o] = uq;
       p.h[o] = hq;
+    }
+  }
+  if constexpr (SHARED) {
+    if (s_unit >= 0) {
+      // Q4_K's lane j takes runs 2 j and 2 j + 1, as these types do; Q2_0 scaled its registers: read them again
+      static_assert(KIND == K_IQ3_S || KIND == K_Q2_0, "the routed type's runs are Q4_K's");
+      if constexpr (KIND == K_Q2_0) read_x(0, x);
+      float sx[RS::kPrepSums + 1];
+      RS::prep_x(x, sx);
+      float g, u;
+      glu_unit<K_Q4_K>(fs, lane, x, x, sx, sx, tab, g, u);
+      if (lane == 0) {
+        const f16 gq = from_f32<f16>(g), uq = from_f32<f16>(u);
+        p.s_h[s_unit] = from_f32<f16>(swiglu_rounded<f16>(gq, uq));
+      }
     }
   }
 }
@@ -666,20 +704,20 @@ bool routed_one_takes(const MatvecParams& p) {
          p.rows <= INT32_MAX / 2;
 }
 
-template <int KIND, int MODE>
+template <int KIND, int MODE, bool SHARED = false>
 int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
   const dim3 block(glu_threads<KIND>());
   switch (upw) {
-    case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MODE>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((routed_glu_kernel<KIND, 2, MODE>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((routed_glu_kernel<KIND, 3, MODE>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((routed_glu_kernel<KIND, 4, MODE>), grid, block, 0, s, p); break;
-    case 6: hipLaunchKernelGGL((routed_glu_kernel<KIND, 6, MODE>), grid, block, 0, s, p); break;
-    case 8: hipLaunchKernelGGL((routed_glu_kernel<KIND, 8, MODE>), grid, block, 0, s, p); break;
-    case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MODE>), grid, block, 0, s, p); break;
-    case 15: hipLaunchKernelGGL((routed_glu_kernel<KIND, 15, MODE>), grid, block, 0, s, p); break;
-    case 16: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MODE>), grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 24, MODE>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((routed_glu_kernel<KIND, 2, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((routed_glu_kernel<KIND, 3, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((routed_glu_kernel<KIND, 4, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL((routed_glu_kernel<KIND, 6, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((routed_glu_kernel<KIND, 8, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 15: hipLaunchKernelGGL((routed_glu_kernel<KIND, 15, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 16: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MODE, SHARED>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 24, MODE, SHARED>), grid, block, 0, s, p); break;
   }
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
@@ -699,7 +737,7 @@ int glu_units_a_wave(int64_t units) {
   return KIND == K_IQ3_S ? 16 : 24;
 }
 
-template <int KIND, int MODE>
+template <int KIND, int MODE, bool SHARED = false>
 int launch_glu_mode(GluParams& p, hipStream_t s) {
   const int64_t units = (int64_t)p.na * p.nb;
   const int upw = glu_units_a_wave<KIND>(units);
@@ -709,7 +747,9 @@ int launch_glu_mode(GluParams& p, hipStream_t s) {
   p.waves = (int)waves;
   p.wave_a = p.waves / p.nb;
   p.wave_b = p.waves % p.nb;
-  return launch_glu_upw<KIND, MODE>(p, upw, dim3((unsigned)(waves / kWaves)), s);
+  // one shared unit a wave at most; above 12 units a wave the shared unit's rows spill registers
+  if (SHARED && (p.s_rows > p.waves || upw > 12)) return STRATA_ERR_SHAPE;
+  return launch_glu_upw<KIND, MODE, SHARED>(p, upw, dim3((unsigned)(waves / kWaves)), s);
 }
 
 template <int KIND>
@@ -732,6 +772,17 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
     p.pairs = mp.pairs;
     p.share = mp.share;
     p.tokens = mp.pairs / mp.share;
+    if (mp.shared[0] != nullptr) {  // the shared expert's gate and up in the same launch: one token
+      if (p.tokens != 1 || mp.shared_rows < 1) return STRATA_ERR_SHAPE;
+      p.s_gate = mp.shared[0];
+      p.s_up = mp.shared[1];
+      p.s_h = reinterpret_cast<f16*>(mp.shared_out);
+      p.s_rows = mp.shared_rows;
+      p.s_row_bytes = mp.shared_row_bytes;
+      p.na = p.pairs;
+      p.nb = p.rows;
+      return launch_glu_mode<KIND, GLU1, true>(p, s);
+    }
     if (p.tokens > 1) {
       p.na = p.pairs;
       p.nb = p.rows;

@@ -209,3 +209,40 @@ def test_q4_k_float32_token_any_range(gpu, scale):
     want = w @ x[0].astype(np.float64)
     assert rel_l2(y, want) <= 1e-5
     assert np.abs(y - want).max() <= 1e-5 * np.abs(w).max() * np.abs(x).max() * np.sqrt(H)
+
+
+# the shared expert's gate and up (Q4_K) in the routed gate/up launch at one token: the routed outputs are the
+# plain launch's bits, the shared h the SwiGLU of the oracle's float64 products (strata_mlx/fused.py:492-493);
+# cases the launch does not take (several tokens, more shared rows than the launch has waves) return None
+@pytest.mark.parametrize("kind,pairs,rows,s_rows", [("IQ3_S", 8, 1536, 1536), ("Q2_0", 8, 1536, 1000),
+                                                    ("IQ3_S", 3, 200, 517), ("IQ3_S", 1, 64, 200)])
+def test_gate_up_with_shared_expert(gpu, kind, pairs, rows, s_rows):
+    from strata_mlx_amd import dense as D
+    experts = 10
+    g = torch.Generator(device=gpu).manual_seed(pairs * 10 + s_rows)
+    gate = B.BlockSwitchLinear(synth.random_stack(kind, experts * rows * H, gpu, g), kind, (experts, rows, H))
+    up = B.BlockSwitchLinear(synth.random_stack(kind, experts * rows * H, gpu, g), kind, (experts, rows, H))
+    sg, su = (D.BlockLinear(synth.random_stack("Q4_K", s_rows * H, gpu, g), "Q4_K", (s_rows, H)) for _ in range(2))
+    rng = np.random.default_rng(rows + s_rows)
+    idx = rng.choice(experts, pairs, replace=False).astype(np.int32)
+    if pairs >= 3:
+        idx[1] = experts + 2  # names no expert
+    x = (rng.standard_normal((1, H)) / 64).astype(np.float16)
+    xs, ix = torch.from_numpy(x).to(gpu), torch.from_numpy(idx).to(gpu)
+    got = B.gate_up_swiglu_shared(gate, up, xs, ix, sg, su)
+    x2 = torch.from_numpy(np.repeat(x, 2, axis=0)).to(gpu)
+    assert B.gate_up_swiglu_shared(gate, up, x2, torch.cat([ix, ix]), sg, su) is None  # two tokens
+    if s_rows > pairs * rows:  # fewer waves than shared rows
+        assert got is None
+        return
+    gs, us, hs, sh = got
+    torch.cuda.synchronize()
+    for a, b in zip((gs, us, hs), B.gate_up_swiglu(gate, up, xs, ix, pairs)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    xd = x.astype(np.float64)[0]
+    gd, ud = (O.dequantize(lay.blocks.cpu().numpy(), "Q4_K", (s_rows, H)).astype(np.float64) @ xd for lay in (sg, su))
+    want = O.swiglu_rounded(gd, ud, np.float16)
+    # g and u within 1e-3 of the float64 products, each rounded to float16, then the SwiGLU's three roundings
+    assert rel_l2(sh.float().cpu().numpy()[0], want) <= 2e-3
+    _, _, hd = D.gate_up_swiglu(sg, su, xs)
+    assert rel_l2(sh.float().cpu().numpy()[0], hd.float().cpu().numpy()[0]) <= 2e-3
