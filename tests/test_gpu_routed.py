@@ -102,8 +102,10 @@ def test_routed_down(gpu, kind, pairs, share, rows, cols):
 
 # (kind, tokens, k, rows): gate/up/SwiGLU at several tokens (the tokens in LDS, units row by row over the pairs)
 # and Q2_0 at one token; experts repeat across tokens as routing makes them repeat
+# (80 pairs: more than a wave has lanes)
 @pytest.mark.parametrize("kind,tokens,k,rows", [("IQ3_S", 4, 8, 1536), ("IQ3_S", 2, 8, 640), ("IQ3_S", 8, 8, 512),
-                                                ("Q2_0", 5, 8, 1536), ("Q2_0", 1, 8, 1536), ("Q2_0", 3, 4, 900)])
+                                                ("Q2_0", 5, 8, 1536), ("Q2_0", 1, 8, 1536), ("Q2_0", 3, 4, 900),
+                                                ("IQ3_S", 8, 10, 256), ("Q2_0", 8, 10, 200)])
 def test_gate_up_tokens(gpu, kind, tokens, k, rows):
     experts = 10
     g = torch.Generator(device=gpu).manual_seed(tokens * 100 + rows)
@@ -114,6 +116,7 @@ def test_gate_up_tokens(gpu, kind, tokens, k, rows):
     rng = np.random.default_rng(tokens * 7 + rows)
     idx = np.stack([rng.choice(experts, k, replace=False) for _ in range(tokens)]).astype(np.int32)
     idx[0, 1] = experts + 3  # names no expert
+    idx[-1, -1] = idx[-1, 0]  # the last token names an expert twice
     x = (rng.standard_normal((tokens, H)) / 64).astype(np.float16)
     gk, uk, hk = (t.cpu().numpy() for t in B.gate_up_swiglu(gate, up, torch.from_numpy(x).to(gpu),
                                                              torch.from_numpy(idx.reshape(-1)).to(gpu), k))
