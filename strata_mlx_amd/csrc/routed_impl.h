@@ -39,10 +39,11 @@ namespace strata_mv {
 constexpr int kGluThreads = 1024;  // sixteen waves a workgroup, one workgroup a CU
 constexpr int kGluWaves = kGluThreads / 64;
 // Q6_K and Q8_0 (a run pair's fields take 18 registers) at eight waves a workgroup: the registers for three units'
-// rows a wave (at sixteen waves, two units' rows spilled)
-template <int KIND>
+// rows a wave (at sixteen waves, two units' rows spilled). Q4_K with a float32 token (mode 3, ONE32) too: a
+// 4096 x 4096 matrix is 2048 units of two rows, which at one a wave fill every CU only at eight waves a workgroup.
+template <int KIND, int MODE = 0>
 constexpr int glu_threads() {
-  return KIND == K_Q6_K || KIND == K_Q8_0 ? 512 : kGluThreads;
+  return KIND == K_Q6_K || KIND == K_Q8_0 || (KIND == K_Q4_K && MODE == 3) ? 512 : kGluThreads;
 }
 constexpr int kGluGroupsPerCU = 1;
 constexpr int kGluMaxUnits = 16;   // units a wave (straight-line code); more units: more waves
@@ -322,8 +323,9 @@ __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], 
 }
 
 template <int KIND, int UPW, int MODE, bool SHARED = false>
-__global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) void routed_glu_kernel(GluParams p) {
-  constexpr int kGluThreads = glu_threads<KIND>(), kGluWaves = kGluThreads / 64;
+__global__ __launch_bounds__((glu_threads<KIND, MODE>()), (glu_threads<KIND, MODE>() / 256)) void routed_glu_kernel(
+    GluParams p) {
+  constexpr int kGluThreads = glu_threads<KIND, MODE>(), kGluWaves = kGluThreads / 64;
   typedef Routed<KIND> R;
   typedef typename R::Fields Fields;
   constexpr bool kOne = MODE == ONE || MODE == ONE32;
@@ -343,13 +345,13 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
   const int gw = blockIdx.x * kGluWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // what the workgroup shares, asked for first: the table entry this thread expands and pieces of the tokens
-  // (ONE32: a quarter of a float32 piece, four values, a thread)
+  // (ONE32: quarters of float32 pieces, four values each: 1024 of them over the workgroup)
   const uint64_t entry = R::fetch(tid);
-  constexpr int kPieceLoads = MODE == ONE32 ? 1 : (512 * kTokens + kGluThreads - 1) / kGluThreads;
+  constexpr int kPieceLoads = MODE == ONE32 ? 1024 / kGluThreads : (512 * kTokens + kGluThreads - 1) / kGluThreads;
   u32x4 xpiece[kPieceLoads];
 #pragma unroll
   for (int k = 0; k < kPieceLoads; ++k)
-    xpiece[k] = p.x[MODE == ONE32 ? tid : min(tid + k * kGluThreads, 512 * p.tokens - 1)];
+    xpiece[k] = p.x[MODE == ONE32 ? tid + k * kGluThreads : min(tid + k * kGluThreads, 512 * p.tokens - 1)];
 
   // the wave's units (pair, row) and whether each is live; ONE: row is the unit's first row (2 i), pair 0
   int pair[UPW], row[UPW];
@@ -409,7 +411,9 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
     // the token's largest magnitude over the workgroup, then the power of two that puts it in [2^14, 2^15)
     uint32_t m = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) m = max(m, xpiece[0][i] & 0x7fffffffu);
+    for (int k = 0; k < kPieceLoads; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = max(m, xpiece[k][i] & 0x7fffffffu);
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, d));
     if (lane == 0) wmax[tid >> 6] = m;
@@ -417,21 +421,25 @@ __global__ __launch_bounds__(glu_threads<KIND>(), glu_threads<KIND>() / 256) voi
 #pragma unroll
     for (int w = 0; w < kGluWaves; ++w) m = max(m, wmax[w]);
     ex = row_exponent(m);
-    // the four values as hi = float16(v / 2^ex) and lo = float16(v / 2^ex - hi): half of float16 piece tid / 2
-    uint32_t hi[2], lo[2];
+    // quarter c's four values as hi = float16(v / 2^ex) and lo = float16(v / 2^ex - hi): half of float16 piece c / 2
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float a = __builtin_ldexpf(__uint_as_float(xpiece[0][2 * i]), -ex);
-      const float b = __builtin_ldexpf(__uint_as_float(xpiece[0][2 * i + 1]), -ex);
-      const f16 ha = from_f32<f16>(a), hb = from_f32<f16>(b);
-      const f16 la = from_f32<f16>(a - (float)ha), lb = from_f32<f16>(b - (float)hb);
-      hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
-      lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+    for (int k = 0; k < kPieceLoads; ++k) {
+      const int c = tid + k * kGluThreads;
+      uint32_t hi[2], lo[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float a = __builtin_ldexpf(__uint_as_float(xpiece[k][2 * i]), -ex);
+        const float b = __builtin_ldexpf(__uint_as_float(xpiece[k][2 * i + 1]), -ex);
+        const f16 ha = from_f32<f16>(a), hb = from_f32<f16>(b);
+        const f16 la = from_f32<f16>(a - (float)ha), lb = from_f32<f16>(b - (float)hb);
+        hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+        lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+      }
+      u32x2* h2 = reinterpret_cast<u32x2*>(xs + x_piece_slot(c >> 1)) + (c & 1);
+      u32x2* l2 = reinterpret_cast<u32x2*>(xs + 512 + x_piece_slot(c >> 1)) + (c & 1);
+      *h2 = u32x2{hi[0], hi[1]};
+      *l2 = u32x2{lo[0], lo[1]};
     }
-    u32x2* h2 = reinterpret_cast<u32x2*>(xs + x_piece_slot(tid >> 1)) + (tid & 1);
-    u32x2* l2 = reinterpret_cast<u32x2*>(xs + 512 + x_piece_slot(tid >> 1)) + (tid & 1);
-    *h2 = u32x2{hi[0], hi[1]};
-    *l2 = u32x2{lo[0], lo[1]};
   } else {
 #pragma unroll
     for (int k = 0; k < kPieceLoads; ++k) {
@@ -706,7 +714,7 @@ bool routed_one_takes(const MatvecParams& p) {
 
 template <int KIND, int MODE, bool SHARED = false>
 int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
-  const dim3 block(glu_threads<KIND>());
+  const dim3 block(glu_threads<KIND, MODE>());
   switch (upw) {
     case 1: hipLaunchKernelGGL((routed_glu_kernel<KIND, 1, MODE, SHARED>), grid, block, 0, s, p); break;
     case 2: hipLaunchKernelGGL((routed_glu_kernel<KIND, 2, MODE, SHARED>), grid, block, 0, s, p); break;
@@ -725,9 +733,9 @@ int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
 
 // Units a wave: the fewest of the forms built that fit the units into one round of resident waves (IQ3_S at two,
 // eight, 15 and 24 units spills registers: three, twelve and 16 instead); at most 24, more waves beyond.
-template <int KIND>
+template <int KIND, int MODE>
 int glu_units_a_wave(int64_t units) {
-  const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * (glu_threads<KIND>() / 64);
+  const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * (glu_threads<KIND, MODE>() / 64);
   const int64_t need = (units + capacity - 1) / capacity;
   static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 15, 16, 24};  // 15: five tokens' 40 pairs on every CU
   for (int f : kForms) {
@@ -740,8 +748,8 @@ int glu_units_a_wave(int64_t units) {
 template <int KIND, int MODE, bool SHARED = false>
 int launch_glu_mode(GluParams& p, hipStream_t s) {
   const int64_t units = (int64_t)p.na * p.nb;
-  const int upw = glu_units_a_wave<KIND>(units);
-  constexpr int kWaves = glu_threads<KIND>() / 64;
+  const int upw = glu_units_a_wave<KIND, MODE>(units);
+  constexpr int kWaves = glu_threads<KIND, MODE>() / 64;
   const int64_t waves = ((units + upw - 1) / upw + kWaves - 1) / kWaves * kWaves;
   if (waves > INT32_MAX) return STRATA_ERR_SHAPE;
   p.waves = (int)waves;
