@@ -725,6 +725,9 @@ int launch_glu_upw(GluParams& p, int upw, dim3 grid, hipStream_t s) {
     case 12: hipLaunchKernelGGL((routed_glu_kernel<KIND, 12, MODE, SHARED>), grid, block, 0, s, p); break;
     case 15: hipLaunchKernelGGL((routed_glu_kernel<KIND, 15, MODE, SHARED>), grid, block, 0, s, p); break;
     case 16: hipLaunchKernelGGL((routed_glu_kernel<KIND, 16, MODE, SHARED>), grid, block, 0, s, p); break;
+    case 20:
+      if constexpr (MODE == ONE) hipLaunchKernelGGL((routed_glu_kernel<KIND, 20, MODE, SHARED>), grid, block, 0, s, p);
+      break;
     default: hipLaunchKernelGGL((routed_glu_kernel<KIND, 24, MODE, SHARED>), grid, block, 0, s, p); break;
   }
   STRATA_CHECK_LAUNCH();
@@ -737,9 +740,12 @@ template <int KIND, int MODE>
 int glu_units_a_wave(int64_t units) {
   const int64_t capacity = (int64_t)device_cus() * kGluGroupsPerCU * (glu_threads<KIND, MODE>() / 64);
   const int64_t need = (units + capacity - 1) / capacity;
-  static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 15, 16, 24};  // 15: five tokens' 40 pairs on every CU
+  // 15: five tokens' 40 pairs on every CU; 20 (one-matrix form only): a Q4_K lm_head's 75968 units of two rows
+  // in 238 workgroups (at 24, 198 of the 256 CUs: 74 against 68 us)
+  static const int kForms[] = {1, 2, 3, 4, 6, 8, 12, 15, 16, 20, 24};
   for (int f : kForms) {
     if (KIND == K_IQ3_S && (f == 2 || f == 8 || f == 15 || f == 24)) continue;
+    if (MODE != ONE && f == 20) continue;
     if (f >= need) return f;
   }
   return KIND == K_IQ3_S ? 16 : 24;

@@ -178,10 +178,12 @@ def test_q4_k_matvec_with_float32_activations(gpu):
         assert rel_l2(got, want) <= REL
 
 
-@pytest.mark.parametrize("kind, rows", [("Q6_K", 4096), ("Q8_0", 4096), ("Q4_K", 1536), ("Q6_K", 151936)])
+@pytest.mark.parametrize("kind, rows", [("Q6_K", 4096), ("Q8_0", 4096), ("Q4_K", 1536), ("Q6_K", 151936),
+                                        ("Q8_0", 20001)])
 def test_dense_decode_layers_of_the_mixed_model(gpu, kind, rows):
     """Config 5's decode: q, k, v (Q6_K), o (Q8_0), the shared expert (Q4_K 1536 x 4096) and lm_head (151936 x 4096
-    Q6_K) at one float16 token, checked on a sample of rows (lm_head) or all of them."""
+    Q6_K) at one float16 token, checked on a sample of rows (lm_head) or all of them; a Q8_0 matrix past 16384 rows
+    (an odd row count) takes the direct kernel as lm_head does."""
     s = Stack(kind, 1, rows, 4096, 400 + rows % 97, gpu)
     x = np.random.default_rng(2).standard_normal((1, 4096)).astype(np.float16)
     layer = D.BlockLinear(s.blocks, kind, (rows, 4096))
