@@ -19,7 +19,7 @@ Beside it, on the same line, the other workloads of the path:
                  1 GB a graph); shared_in_routed: the shared expert's gate and up taken by the headline layers'
                  routed gate+up launches instead (its marginal time over those launches alone)
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
-                 the dense layers as tile products, TFLOPS
+                 the dense layers dequantized for the chunk and multiplied by the library product, TFLOPS
   roofline       the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
                  (HIP events around a graph of those launches only), against 8 TB/s
   cpu_baseline   the oracle's numpy decode of the touched experts (one thread) + float32 matvecs (BLAS on the
@@ -359,7 +359,8 @@ def q4k_bench(B, synth, dev, steps, warmup, copies=64):
 def prefill_bench(B, D, synth, dev, lins, steps, warmup, rng, tokens=2048):
     """A 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts of `lins` (Zipf top-8) through
     the tiles, and the dense layers (q, k, v Q6_K fused, o Q8_0, the shared expert's Q4_K gate and up fused, down) as
-    tile products of the whole chunk. Returns TFLOPS over the real products' flops, each part and all."""
+    the reference multiplies a prompt chunk: each dequantized for the chunk, then the library product. Returns
+    TFLOPS over the real products' flops, each part and all."""
     g = torch.Generator(device=dev)
     g.manual_seed(4)
     mk = lambda kind, r, c: D.BlockLinear(synth.random_stack(kind, r * c, dev, g), kind, (r, c))

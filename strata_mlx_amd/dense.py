@@ -9,10 +9,11 @@
     BlockEmbedding rows of an embedding decoded when their tokens come (dense.py:245-258).
 
 Up to MAX_TOKENS tokens a product is a window of the matvec kernel (each block decoded once for every token). A
-longer chunk (a prompt's) goes through the tile kernels as a stack of one matrix: its tokens in tiles of 16, every
-weight tile decoded into LDS once for 16 tiles and multiplied on MFMA with float32 sums (the reference multiplies
-float weights kept for the purpose, dense.py:141-157; here no float copy of the layer is made). bfloat16 tokens
-are scaled into float16 rows by a power of two each, exactly, and the sums scaled back.
+longer chunk (a prompt's) of float16 or bfloat16 tokens is multiplied as the reference multiplies it
+(dense.py:234-241): the layer dequantized for the chunk (strata_dequantize, each weight exact in float32 and
+rounded once to float16) and let go, then a library product with float32 sums (torch.mm; 4-6 times the tile
+kernels' speed at 2048 tokens). bfloat16 tokens are scaled into float16 rows by a power of two each, exactly, and
+the sums scaled back. float32 tokens go through the tile kernels as a stack of one matrix (exact weights on MFMA).
 """
 
 import torch
@@ -93,11 +94,29 @@ class BlockLinear:
                 out = out[:, row_ids.reshape(-1).long()]
         elif tokens <= MAX_TOKENS or row_ids is not None:
             out = B.window_matvec(self.blocks, self.kind, rows, cols, x2, row_ids=row_ids)
+        elif x2.dtype in (torch.float16, torch.bfloat16):
+            out = float16_chunk(self.floats(torch.float16), x2)
         elif B.tileable(self.kind, rows, cols):
             out = tiled_chunk(self.blocks, self.kind, rows, cols, x2)
         else:
             out = x2 @ self.floats(x.dtype).T
         return out.reshape(*lead, out.shape[-1])
+
+
+def float16_chunk(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """x (tokens, cols) float16 or bfloat16 times float16 weights w (rows, cols), as the reference multiplies a
+    prompt chunk (dense.py:234-241: the weights unpacked for the chunk, then a library product): float32 sums,
+    (tokens, rows) in x's type. bfloat16 rows are scaled into float16 by a power of two each (rows_to_f16: exact),
+    and the sums scaled back."""
+    if x.dtype == torch.float16:
+        return torch.mm(x, w.t(), out_dtype=torch.float32).to(torch.float16)
+    x16, x_max = B.rows_to_f16(x)
+    m = x_max.view(torch.float32)
+    _, ex = torch.frexp(m)
+    # the power of two rows_to_f16 divided by: floor(log2 max) - 14 (0 for a row of zeros, infinities or NaN)
+    e = torch.where((m > 0) & torch.isfinite(m), ex - 15, torch.zeros_like(ex))
+    out = torch.mm(x16, w.t(), out_dtype=torch.float32)
+    return torch.ldexp(out, e[:, None].to(torch.float32)).to(x.dtype)
 
 
 def tiled_chunk(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor) -> torch.Tensor:

@@ -258,6 +258,31 @@ def test_prefill_dense_layers(gpu, kind, rows, cols, dtype):
     assert rel_l2(got[:, pick], as_dtype(want, dtype)) <= REL
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_dense_layer_in_a_graph(gpu, dtype):
+    """The prompt-chunk product (the layer dequantized, then the library product) captured in a HIP graph, as the
+    benchmark runs it: every replay, with eager work between them, gives the eager call's bits."""
+    s = Stack("Q6_K", 1, 1024, 4096, 611, gpu)
+    layer = D.BlockLinear(s.blocks, "Q6_K", (1024, 4096))
+    x = torch.from_numpy(np.random.default_rng(8).standard_normal((512, 4096)).astype(np.float32)).to(dtype).to(gpu)
+    want = layer(x)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        layer(x)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = layer(x)
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {r}"
+        layer(x * 2)  # eager work between the replays
+        torch.cuda.synchronize()
+
+
 def test_matvec_separate_against_the_oracle(gpu):
     """matvec_separate (blocks.py:331-346): every pair brings its expert's blocks as a tensor of its own; 1536 x 4096
     IQ3_S experts, one token shared by eight pairs and a row for each pair, against the oracle."""
