@@ -131,6 +131,14 @@ int strata_route_tiles(const uint32_t* idx, int64_t pairs, int64_t k, int64_t ex
 int strata_rows_to_f16(const void* a, int64_t rows, int64_t cols, int a_dtype, void* out, uint32_t* row_max,
                        void* stream);
 
+/* The inverse of strata_rows_to_f16's scaling, for products of the scaled rows: out[r, c] = c[r, c] * 2^e(r) rounded
+ * once to out_dtype (BF16, F16 or F32), e(r) from row_max[r] as strata_rows_to_f16 set it; c float32 (rows, cols),
+ * out (rows, cols), at most 65535 rows. No counterpart in the reference, which multiplies a prompt chunk's
+ * bfloat16 tokens by weights in bfloat16 (strata_mlx/dense.py:234-241): here the tokens are scaled into float16
+ * exactly, multiplied by float16 weights with float32 sums, and their sums come back through this call. */
+int strata_rows_from_f32(const float* c, int64_t rows, int64_t cols, const uint32_t* row_max, int out_dtype,
+                         void* out, void* stream);
+
 /* strata_route_tiles with its workspace in the library's own device memory (a file-scope array of about 1 MB a
  * GPU, held until the process ends): the call allocates nothing, for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. pairs at

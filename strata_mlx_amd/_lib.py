@@ -53,6 +53,7 @@ SIGNATURES = {
     "strata_route_tiles_noalloc": (_i, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p]),
     "strata_grouped_matmul": (_i, [_i, _p, _i64, _i64, _i64, _p, _i, _p, _p, _i64, _i64, _p, _p]),
     "strata_rows_to_f16": (_i, [_p, _i64, _i64, _i, _p, _p, _p]),
+    "strata_rows_from_f32": (_i, [_p, _i64, _i64, _p, _i, _p, _p]),
     "strata_prompt_gate_up_swiglu": (_i, [_i, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _i, _p]),
     "strata_prompt_down": (_i, [_i, _p, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _i64, _p, _i, _p]),
 }

@@ -525,6 +525,21 @@ def rows_to_f16(a: torch.Tensor) -> tuple:
     return out, row_max
 
 
+def rows_from_f32(c: torch.Tensor, row_max: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Products of rows scaled by rows_to_f16 (c float32 (rows, cols), row_max its second output) scaled back by
+    each row's power of two and rounded once to `dtype`."""
+    c = c.contiguous()
+    _lib.require_device(c)
+    rows, cols = c.shape
+    out = torch.empty((rows, cols), dtype=dtype, device=c.device)
+    for r0 in range(0, rows, 65535):  # the launch takes 65535 rows at a time
+        n = min(65535, rows - r0)
+        _lib.check(_lib.library().strata_rows_from_f32(c[r0:].data_ptr(), n, cols, row_max[r0:].data_ptr(),
+                                                       _lib.dtype_id(dtype), out[r0:].data_ptr(), _lib.stream()),
+                   "rows_from_f32")
+    return out
+
+
 def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, tile_expert: torch.Tensor,
                 out: torch.Tensor | None = None) -> torch.Tensor:
     """out[p] = W[expert of p's tile] . a[p] for a stack `blocks` of `shape` (experts, rows, cols), on MFMA.

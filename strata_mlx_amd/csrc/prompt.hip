@@ -36,6 +36,28 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_f16_kernel(const AT* a, i
   if (threadIdx.x == 0) row_max[r] = m;
 }
 
+// The products of rows scaled by rows_to_f16 scaled back, out[r, c] = c[r, c] * 2^e(r), rounded once to OT: four
+// values a thread (one 16-byte load where a row's length is a multiple of four), a row of blocks a row.
+template <typename OT>
+__global__ __launch_bounds__(256) void rows_from_f32_kernel(const float* c, int cols, const uint32_t* row_max,
+                                                            OT* out) {
+  const int64_t r = blockIdx.y;
+  const int ex = row_exponent(row_max[r]);
+  const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= cols) return;
+  const float* src = c + r * cols + i;
+  OT* dst = out + r * cols + i;
+  if ((cols & 3) == 0) {
+    const float4 v = *reinterpret_cast<const float4*>(src);
+    dst[0] = from_f32<OT>(__builtin_ldexpf(v.x, ex));
+    dst[1] = from_f32<OT>(__builtin_ldexpf(v.y, ex));
+    dst[2] = from_f32<OT>(__builtin_ldexpf(v.z, ex));
+    dst[3] = from_f32<OT>(__builtin_ldexpf(v.w, ex));
+  } else {
+    for (int j = 0; j < 4 && i + j < cols; ++j) dst[j] = from_f32<OT>(__builtin_ldexpf(src[j], ex));
+  }
+}
+
 // Rows of y for the pairs naming no expert: NaN, as every matvec gives them.
 template <typename OT>
 __global__ __launch_bounds__(256) void nan_rows_kernel(const uint32_t* idx, int64_t experts, int cols, OT* y) {
@@ -80,6 +102,25 @@ void fill_shape(PromptParams& p, int kind, int64_t experts, int64_t rows, int64_
 }  // namespace strata_prompt
 
 using namespace strata_prompt;
+
+extern "C" int strata_rows_from_f32(const float* c, int64_t rows, int64_t cols, const uint32_t* row_max, int out_dtype,
+                                    void* out, void* stream) {
+  if (rows < 0 || cols < 0 || cols > (1 << 28) || rows > 65535) return STRATA_ERR_SHAPE;
+  if (rows == 0 || cols == 0) return STRATA_OK;
+  if (!c || !row_max || !out) return STRATA_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((cols + 1023) / 1024), (unsigned)rows);
+  if (out_dtype == DT_BF16)
+    hipLaunchKernelGGL((rows_from_f32_kernel<bf16_t>), grid, dim3(256), 0, s, c, (int)cols, row_max, (bf16_t*)out);
+  else if (out_dtype == DT_F16)
+    hipLaunchKernelGGL((rows_from_f32_kernel<f16>), grid, dim3(256), 0, s, c, (int)cols, row_max, (f16*)out);
+  else if (out_dtype == DT_F32)
+    hipLaunchKernelGGL((rows_from_f32_kernel<float>), grid, dim3(256), 0, s, c, (int)cols, row_max, (float*)out);
+  else
+    return STRATA_ERR_DTYPE;
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
 
 extern "C" int strata_rows_to_f16(const void* a, int64_t rows, int64_t cols, int a_dtype, void* out, uint32_t* row_max,
                                   void* stream) {

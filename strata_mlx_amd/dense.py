@@ -109,14 +109,9 @@ def float16_chunk(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     (tokens, rows) in x's type. bfloat16 rows are scaled into float16 by a power of two each (rows_to_f16: exact),
     and the sums scaled back."""
     if x.dtype == torch.float16:
-        return torch.mm(x, w.t(), out_dtype=torch.float32).to(torch.float16)
+        return torch.mm(x, w.t())  # float32 sums, rounded once to float16
     x16, x_max = B.rows_to_f16(x)
-    m = x_max.view(torch.float32)
-    _, ex = torch.frexp(m)
-    # the power of two rows_to_f16 divided by: floor(log2 max) - 14 (0 for a row of zeros, infinities or NaN)
-    e = torch.where((m > 0) & torch.isfinite(m), ex - 15, torch.zeros_like(ex))
-    out = torch.mm(x16, w.t(), out_dtype=torch.float32)
-    return torch.ldexp(out, e[:, None].to(torch.float32)).to(x.dtype)
+    return B.rows_from_f32(torch.mm(x16, w.t(), out_dtype=torch.float32), x_max, x.dtype)
 
 
 def tiled_chunk(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor) -> torch.Tensor:
