@@ -36,6 +36,56 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_f16_kernel(const AT* a, i
   if (threadIdx.x == 0) row_max[r] = m;
 }
 
+// rows_to_f16 for 16-bit rows of at most 8192 values, a multiple of 8: the row read once, 16 bytes (8 values) a
+// piece and up to CH pieces a thread held in registers between the row's maximum and the scaled stores.
+template <typename AT, int CH>
+__global__ __launch_bounds__(kRowThreads) void rows_to_f16_vec_kernel(const AT* a, int cols, f16* out,
+                                                                      uint32_t* row_max) {
+  static_assert(sizeof(AT) == 2, "16-bit rows");
+  __shared__ uint32_t wmax[kRowThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int pieces = cols / 8;
+  const u32x4* src = reinterpret_cast<const u32x4*>(a + r * cols);
+  u32x4 v[CH];
+  uint32_t m = 0;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c = threadIdx.x + k * kRowThreads;
+    v[k] = c < pieces ? src[c] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const AT lo = __builtin_bit_cast(AT, (uint16_t)(v[k][i] & 0xffffu));
+      const AT hi = __builtin_bit_cast(AT, (uint16_t)(v[k][i] >> 16));
+      m = max(m, __float_as_uint(to_f32(lo)) & 0x7fffffffu);
+      m = max(m, __float_as_uint(to_f32(hi)) & 0x7fffffffu);
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, d));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kRowThreads / 64; ++w) m = max(m, wmax[w]);
+  const int ex = row_exponent(m);
+  u32x4* dst = reinterpret_cast<u32x4*>(out + r * cols);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c = threadIdx.x + k * kRowThreads;
+    if (c < pieces) {
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const AT lo = __builtin_bit_cast(AT, (uint16_t)(v[k][i] & 0xffffu));
+        const AT hi = __builtin_bit_cast(AT, (uint16_t)(v[k][i] >> 16));
+        o[i] = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<f16>(__builtin_ldexpf(to_f32(lo), -ex))) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<f16>(__builtin_ldexpf(to_f32(hi), -ex))) << 16);
+      }
+      dst[c] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+  if (threadIdx.x == 0) row_max[r] = m;
+}
+
 // The products of rows scaled by rows_to_f16 scaled back, out[r, c] = c[r, c] * 2^e(r), rounded once to OT: four
 // values a thread (one 16-byte load where a row's length is a multiple of four), a row of blocks a row.
 template <typename OT>
@@ -128,6 +178,31 @@ extern "C" int strata_rows_to_f16(const void* a, int64_t rows, int64_t cols, int
   if (rows == 0 || cols == 0) return STRATA_OK;
   if (!a || !out || !row_max) return STRATA_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
+  // 16-bit rows of at most 8192 values, a multiple of 8, at 16-byte aligned addresses: read once, 16 bytes a load
+  const bool vec = (a_dtype == DT_BF16 || a_dtype == DT_F16) && cols % 8 == 0 && cols <= 8 * 4 * kRowThreads &&
+                   ((uintptr_t)a & 15) == 0 && ((uintptr_t)out & 15) == 0;
+  if (vec) {
+    const int ch = (int)((cols / 8 + kRowThreads - 1) / kRowThreads);  // pieces a thread: 1 to 4
+    auto go = [&](auto tag, auto chc) {
+      typedef decltype(tag) AT;
+      hipLaunchKernelGGL((rows_to_f16_vec_kernel<AT, decltype(chc)::value>), dim3((unsigned)rows), dim3(kRowThreads),
+                         0, s, (const AT*)a, (int)cols, (f16*)out, row_max);
+    };
+    auto by_ch = [&](auto tag) {
+      switch (ch) {
+        case 1: go(tag, std::integral_constant<int, 1>()); break;
+        case 2: go(tag, std::integral_constant<int, 2>()); break;
+        case 3: go(tag, std::integral_constant<int, 3>()); break;
+        default: go(tag, std::integral_constant<int, 4>()); break;
+      }
+    };
+    if (a_dtype == DT_BF16)
+      by_ch(bf16_t{});
+    else
+      by_ch(f16{});
+    STRATA_CHECK_LAUNCH();
+    return STRATA_OK;
+  }
   if (a_dtype == DT_BF16)
     hipLaunchKernelGGL((rows_to_f16_kernel<bf16_t>), dim3((unsigned)rows), dim3(kRowThreads), 0, s,
                        (const bf16_t*)a, (int)cols, (f16*)out, row_max);
