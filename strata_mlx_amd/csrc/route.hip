@@ -38,18 +38,42 @@ __global__ __launch_bounds__(1024) void route_scan(uint32_t* blk, int nblocks, i
                                                   uint32_t* first_tile, uint32_t* tile_expert, uint32_t* token,
                                                   uint32_t* slot_pair) {
   extern __shared__ uint32_t sh[];  // tiles per expert, then their scan: [experts + 1]
-  const int tid = threadIdx.x, nt = blockDim.x;
+  __shared__ uint32_t wsum[1024 / 64];
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < experts; e += nt) {
+    // the expert's count in each block of pairs, 16 blocks' loads at a time, then their running sums stored back
     uint32_t run = 0;
-    for (int b = 0; b < nblocks; ++b) {
-      const uint32_t v = blk[(int64_t)b * experts + e];
-      blk[(int64_t)b * experts + e] = run;
-      run += v;
+    for (int b0 = 0; b0 < nblocks; b0 += 16) {
+      uint32_t v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = b0 + i < nblocks ? blk[(int64_t)(b0 + i) * experts + e] : 0u;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (b0 + i < nblocks) blk[(int64_t)(b0 + i) * experts + e] = run;
+        run += v[i];
+      }
     }
     sh[e] = (run + tile - 1) / tile;
   }
   __syncthreads();
-  if (tid == 0) {  // exclusive scan of the tile counts; experts <= 65536, a few microseconds at most
+  if (experts <= nt) {  // exclusive scan of the tile counts over the workgroup: a wave's, then the waves' totals
+    const uint32_t own = tid < experts ? sh[tid] : 0u;
+    uint32_t v = own;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t t = (uint32_t)__shfl_up((int)v, d);
+      if (lane >= d) v += t;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    uint32_t total = 0;
+    for (int w = 0; w < nt / 64; ++w) total += wsum[w];
+    __syncthreads();  // every thread has read its count
+    if (tid < experts) sh[tid] = before + v - own;
+    if (tid == 0) sh[experts] = total;
+  } else if (tid == 0) {  // more experts than threads: one thread's scan
     uint32_t run = 0;
     for (int e = 0; e < experts; ++e) {
       const uint32_t v = sh[e];
