@@ -229,7 +229,8 @@ __device__ __forceinline__ float decode_pair(const RunPair<KIND>& f, int h, int 
     for (int l = 0; l < 8; ++l) {
       const u32x2 g = t.grid[((l < 4 ? qs0 : qs1) >> (8 * (l & 3))) & 255];
       const uint32_t s7 = (aux >> (7 * (l >> 1))) & 127;
-      const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);  // ksigns: the parity in bit 7
+      // ksigns: the parity in bit 7 (the count's bit 0; its bits 1-2 land in bits 8-9, which the nibbles leave out)
+      const uint32_t s8 = s7 | ((uint32_t)__builtin_popcount(s7) << 7);
       const u32x2 m = t.sign4[(s8 >> (4 * (l & 1))) & 15];
       w[2 * l] = g[0] ^ m[0];
       w[2 * l + 1] = g[1] ^ m[1];

@@ -1,9 +1,9 @@
 // The prompt kernels: grouped dequant-matmuls over tiles of 16 slots, each tile one expert's, on CDNA4 MFMA, for
 // IQ3_S, IQ3_XXS and Q2_0 rows of whole 256-weight steps and float16 activations (strata_mlx/blocks.py:583-694).
 //
-// c[s, :] = W[e(s)] . a[s, :]. A workgroup (4 waves) takes a chunk, the tiles of one expert within an aligned
-// window of NT = 2 tiles (the workgroup at the chunk's first tile works, the others exit at once), and a block of
-// rows. Every wave holds two groups of 16 rows: in the SwiGLU form the same 16 rows of gate and of up, otherwise 32
+// c[s, :] = W[e(s)] . a[s, :]. A workgroup (4 waves) takes a chunk, up to NT = 3 consecutive tiles of one expert
+// (a run of one expert's tiles is cut into chunks of NT from its first tile; the workgroup at a chunk's first tile
+// works, the others exit at once), and a block of rows. Every wave holds two groups of 16 rows: in the SwiGLU form the same 16 rows of gate and of up, otherwise 32
 // rows of one matrix. The expert's rows are decoded once for all tiles of the chunk, and the body is compiled for
 // each chunk size, so no branch sits between the MFMAs.
 //
@@ -24,8 +24,8 @@
 // magnitude, and the sums are scaled back by that power exactly.
 //
 // Workgroup i runs on XCD i % 8. Windows of NT tiles go to the XCDs in turn, and every row block of a window's
-// tiles runs on the window's XCD: the chunks (one or two a window) spread evenly over the XCDs, and a tile's
-// activations are read into one L2.
+// tiles runs on the window's XCD: the chunks (at most NT starting in a window) spread evenly over the XCDs, and a
+// chunk's activations are read into one L2 (its workgroups are those of its first tile).
 #pragma once
 #include "direct_impl.h"
 
@@ -58,9 +58,9 @@ struct PromptParams {
   int rows, cols, row_bytes, n_tiles, row_blocks;
 };
 
-// The run's own scale folded into its 16 packed float16 pairs of integers (exact, see above).
+// The run's own scale, as a float16 pair: IQ3_S 1 + 2s, IQ3_XXS 2s + 1, Q2_0 d.
 template <int KIND>
-__device__ __forceinline__ void fold_run(const RunPair<KIND>& f, int h, int g, uint32_t (&w)[16]) {
+__device__ __forceinline__ h2v run_scale2(const RunPair<KIND>& f, int h, int g) {
   f16 m;
   if constexpr (KIND == K_IQ3_S) {
     m = (f16)(float)(1 + 2 * __builtin_amdgcn_ubfe((uint32_t)f.sc, 8 * (g & 1) + 4 * h, 4));
@@ -69,9 +69,15 @@ __device__ __forceinline__ void fold_run(const RunPair<KIND>& f, int h, int g, u
   } else {
     m = __builtin_bit_cast(f16, (uint16_t)f.d);
   }
-  const h2v m2 = h2v{m, m};
+  return h2v{m, m};
+}
+
+// The run's own scale folded into N packed float16 pairs of integers (exact, see above).
+template <int KIND, int N>
+__device__ __forceinline__ void fold_run(const RunPair<KIND>& f, int h, int g, uint32_t (&w)[N]) {
+  const h2v m2 = run_scale2<KIND>(f, h, g);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) w[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, w[i]) * m2);
+  for (int i = 0; i < N; ++i) w[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, w[i]) * m2);
 }
 
 // What multiplies a row's whole step: IQ3_S d, IQ3_XXS d / 4 (strata_mlx/blocks.py:89-116); Q2_0 has none left.
@@ -102,41 +108,51 @@ __device__ __forceinline__ void put_signs(uint32_t s8, const u32x2& g0, const u3
   w[3] = (m3 & 0x80008000u) | g1[1];
 }
 
+// Group pair l (weights 8 l .. 8 l + 7) of run h of the lane's run pair g, IQ3_XXS or IQ3_S: 4 packed float16
+// pairs, the run's scale and signs folded in (exact). What the four group pairs of a run share is the same
+// expression for each, computed once where they are unrolled together.
+template <int KIND>
+__device__ __forceinline__ void decode_folded4(const RunPair<KIND>& f, int h, int g, int l, uint32_t (&w)[4],
+                                               const DirectTables<KIND>& t) {
+  static_assert(KIND == K_IQ3_XXS || KIND == K_IQ3_S, "the codebook types");
+  if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116: groups 2l, 2l + 1, signs ksigns[7 bits of aux]
+    const uint32_t q = f.qs[2 * h + (l >> 1)];
+    const u32x2 g0 = t.grid[(q >> (16 * (l & 1))) & 255];
+    const u32x2 g1 = t.grid[(q >> (16 * (l & 1) + 8)) & 255];
+    const uint32_t s7 = __builtin_amdgcn_ubfe(f.aux[h], 7 * l, 7);
+    // the parity in bit 7: the count's bit 0 (its bits 1-2 land in bits 8-9, which put_signs shifts out of both
+    // 16-bit halves)
+    const uint32_t s8 = s7 | ((uint32_t)__builtin_popcount(s7) << 7);
+    put_signs(s8, g0, g1, w);
+  } else {  // strata_mlx/blocks.py:89-102: groups 2l, 2l + 1, their ninth index bits from qh, signs byte l
+    const uint32_t qs = f.qs[2 * h + (l >> 1)];
+    const uint32_t qh = (f.qh >> (8 * h)) & 255;
+    const uint32_t hb = (__builtin_amdgcn_ubfe(qh, 4 * (l >> 1), 4) * 0x204081u) & 0x01010101u;
+    const uint32_t iw = __builtin_amdgcn_perm(hb, qs, (l & 1) ? 0x07030602u : 0x05010400u);
+    const uint32_t three = 3;
+    const u32x2 g0 = strata_mv::lds_entry(t.grid, strata_mv::word_shl<0>(iw, three));
+    const u32x2 g1 = strata_mv::lds_entry(t.grid, strata_mv::word_shl<1>(iw, three));
+    put_signs((f.sg[h] >> (8 * l)) & 255u, g0, g1, w);
+  }
+  fold_run<KIND, 4>(f, h, g, w);
+}
+
 // Run h of the lane's run pair g: 16 packed float16 pairs, the run's scale and signs folded in (exact).
 template <int KIND>
 __device__ __forceinline__ void decode_folded(const RunPair<KIND>& f, int h, int g, uint32_t (&w)[16],
                                               const DirectTables<KIND>& t) {
-  if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116
-    const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
-    const uint32_t aux = f.aux[h];
+  if constexpr (KIND == K_IQ3_XXS || KIND == K_IQ3_S) {
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {  // group pair l: groups 2l, 2l + 1, signs ksigns[7 bits of aux]
-      const uint32_t q = l < 2 ? qs0 : qs1;
-      const u32x2 g0 = t.grid[(q >> (16 * (l & 1))) & 255];
-      const u32x2 g1 = t.grid[(q >> (16 * (l & 1) + 8)) & 255];
-      const uint32_t s7 = __builtin_amdgcn_ubfe(aux, 7 * l, 7);
-      const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);  // the parity in bit 7
-      put_signs(s8, g0, g1, w + 4 * l);
-    }
-  } else if constexpr (KIND == K_IQ3_S) {  // strata_mlx/blocks.py:89-102
-    const uint32_t qs0 = f.qs[2 * h], qs1 = f.qs[2 * h + 1];
-    const uint32_t qh = (f.qh >> (8 * h)) & 255, sg = f.sg[h];
-    const uint32_t hb0 = (__builtin_amdgcn_ubfe(qh, 0, 4) * 0x204081u) & 0x01010101u;
-    const uint32_t hb1 = (__builtin_amdgcn_ubfe(qh, 4, 4) * 0x204081u) & 0x01010101u;
-    const uint32_t i01 = __builtin_amdgcn_perm(hb0, qs0, 0x05010400u), i23 = __builtin_amdgcn_perm(hb0, qs0, 0x07030602u);
-    const uint32_t i45 = __builtin_amdgcn_perm(hb1, qs1, 0x05010400u), i67 = __builtin_amdgcn_perm(hb1, qs1, 0x07030602u);
-    const uint32_t three = 3;
+    for (int l = 0; l < 4; ++l) {
+      uint32_t w4[4];
+      decode_folded4<KIND>(f, h, g, l, w4, t);
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {  // group pair l: groups 2l, 2l + 1 (index words i01 .. i67), signs byte l
-      const uint32_t iw = l == 0 ? i01 : l == 1 ? i23 : l == 2 ? i45 : i67;
-      const u32x2 g0 = strata_mv::lds_entry(t.grid, strata_mv::word_shl<0>(iw, three));
-      const u32x2 g1 = strata_mv::lds_entry(t.grid, strata_mv::word_shl<1>(iw, three));
-      put_signs((sg >> (8 * l)) & 255u, g0, g1, w + 4 * l);
+      for (int i = 0; i < 4; ++i) w[4 * l + i] = w4[i];
     }
   } else {
     strata_mv::decode_run<KIND>(f, h, g, w, t);
+    fold_run<KIND, 16>(f, h, g, w);
   }
-  fold_run<KIND>(f, h, g, w);
 }
 
 // Column (within the step) of the first of the 8 weights lane group g gives MFMA (h, q): run run_of(g, h), its
@@ -324,11 +340,13 @@ __device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTab
 // field that starts 2 or 4 bytes past such a boundary is put together in registers (v_alignbyte).
 //
 // One row buffer a wave: the next step's rows are asked for as soon as this step's fields are in registers, and
-// arrive while they are decoded. Two activation buffers: one workgroup barrier a step. The loads are inline
-// assembly, so the compiler places no wait of its own for them: the one wait (vmcnt(0)) comes at the top of each
-// step, and the barriers wait only for LDS (a __syncthreads would also wait for the next step's rows). The LDS
-// (50-52 KB) and the registers leave three workgroups on a CU; at two (a third row buffer, or the IQ3_XXS codebook
-// with its signs folded in, 32 KB) or at four (128 registers, spilled) the kernel ran slower.
+// arrive while they are decoded. Chunks of up to three tiles take one activation buffer and two workgroup barriers a
+// step (the kernels built for chunks of at most two take two buffers and one barrier; two buffers of three tiles
+// would leave two workgroups a CU). The loads are inline assembly, so the compiler places no wait of its own for
+// them: the one wait (vmcnt(0)) comes at the top of each step, and the barriers wait only for LDS (a __syncthreads
+// would also wait for the next step's rows). The LDS (42-44 KB) and the registers (159-167) leave three workgroups
+// on a CU; at two (a third row buffer, or the IQ3_XXS codebook with its signs folded in, 32 KB) or at four (128
+// registers, spilled) the kernel ran slower.
 template <int KIND>
 constexpr bool kStagedKind = KIND == K_IQ3_S || KIND == K_IQ3_XXS;
 template <int KIND>
@@ -388,6 +406,13 @@ __device__ __forceinline__ void lds_fields(const uint8_t* slot, int g, RunPair<K
   }
 }
 
+// Activation buffers of the staged form: two (one barrier a step) up to chunks of two tiles; for longer chunks one,
+// which keeps the LDS at three workgroups a CU (a second barrier a step waits for its writes).
+template <int NT>
+constexpr int activation_buffers() {
+  return NT <= 2 ? 2 : 1;
+}
+
 template <int KIND, int MODE, typename OT, int WAVES, int NT, int NTC>
 __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const DirectTables<KIND>& tab,
                                                  f16* a_lds, uint8_t* w_lds, uint32_t e, int t0, int rb, int tid,
@@ -401,6 +426,7 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
   static_assert(kStagedKind<KIND>, "staged rows: IQ3_S, IQ3_XXS");
   constexpr int kSB = kStepBytes<KIND>, kDW = kSlotDwords<KIND>, kGL = kGroupLoads;
   constexpr int kABuf = NT * 16 * kPitch;  // float16: an activation buffer
+  constexpr int kABufs = activation_buffers<NT>();
   const int lane = tid & 63;
 
   const int n = lane & 15, g = lane >> 4;
@@ -448,10 +474,12 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
   u32x4 av[kLoads];
 #pragma unroll
   for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q]);
+  if constexpr (kABufs == 2) {
 #pragma unroll
-  for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+    for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
+  }
   stage(0);
-  if (nsteps > 1) {
+  if (kABufs == 2 && nsteps > 1) {
 #pragma unroll
     for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + kStep);
   }
@@ -465,11 +493,19 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
     for (int sp = 0; sp < 2; ++sp) {
       const int k = kb + sp;
       if (k < nsteps) {
-        wait_loads();   // this wave's rows of step k and its activation pieces of step k + 1
-        lds_barrier();  // every wave's activations of step k are written and every wave is done with step k - 1
-        if (k + 1 < nsteps) {
+        // two buffers: this wave's rows of step k and its activation pieces of step k + 1 are in, every wave's
+        // activations of step k are written and every wave is done with step k - 1; one buffer: the pieces of
+        // step k are in, and every wave is done reading step k - 1's
+        wait_loads();
+        lds_barrier();
+        if constexpr (kABufs == 2) {
+          if (k + 1 < nsteps) {
 #pragma unroll
-          for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + (sp ^ 1) * kABuf + adst[q]) = av[q];
+            for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + (sp ^ 1) * kABuf + adst[q]) = av[q];
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4*>(a_lds + adst[q]) = av[q];
         }
         RunPair<KIND> f[2];
 #pragma unroll
@@ -485,40 +521,58 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           stage(k + 1);
         }
-        if (k + 2 < nsteps) {
+        if (k + kABufs < nsteps) {
 #pragma unroll
-          for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + 2) * kStep);
+          for (int q = 0; q < kLoads; ++q) av[q] = *reinterpret_cast<const u32x4*>(arow[q] + (k + kABufs) * kStep);
         }
-        const f16* ab = a_lds + sp * kABuf;
+        if constexpr (kABufs == 1) lds_barrier();  // every wave's activations of step k are written
+        const f16* ab = a_lds + (kABufs == 2 ? sp * kABuf : 0);
 
         f32x4 part[2][NTC];
 #pragma unroll
         for (int i = 0; i < NTC; ++i) part[0][i] = part[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // Two forms of a run's work. Whole: both row groups' runs decoded at once, two MFMA groups' activations
+        // read ahead of the decode and two after it. Interleaved (chunks of three tiles, whose registers the whole
+        // form overruns): group pair q of both runs decoded just before MFMA group q, whose activations are read
+        // while group q - 1 multiplies.
+        constexpr bool kInterleaved = NTC >= 3;
+        auto read_a = [&](f16x8 (&a8)[4][NTC], int h, int q) {
+#pragma unroll
+          for (int i = 0; i < NTC; ++i)
+            a8[q][i] = *reinterpret_cast<const f16x8*>(ab + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
+        };
+        auto mfma_group = [&](const f16x8 (&a8)[NTC], const uint32_t* w0, const uint32_t* w1) {
+          const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[0], w0[1], w0[2], w0[3]});
+          const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[0], w1[1], w1[2], w1[3]});
+#pragma unroll
+          for (int i = 0; i < NTC; ++i) {
+            part[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[i], b0, part[0][i], 0, 0, 0);
+            part[1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[i], b1, part[1][i], 0, 0, 0);
+          }
+        };
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           f16x8 a8[4][NTC];
+          if constexpr (kInterleaved) {
+            read_a(a8, h, 0);
 #pragma unroll
-          for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int i = 0; i < NTC; ++i)
-              a8[q][i] = *reinterpret_cast<const f16x8*>(ab + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
-          uint32_t w0[16], w1[16];
-          decode_folded<KIND>(f[0], h, g, w0, tab);
-          decode_folded<KIND>(f[1], h, g, w1, tab);
-#pragma unroll
-          for (int q = 2; q < 4; ++q)
-#pragma unroll
-            for (int i = 0; i < NTC; ++i)
-              a8[q][i] = *reinterpret_cast<const f16x8*>(ab + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[4 * q], w0[4 * q + 1], w0[4 * q + 2], w0[4 * q + 3]});
-            const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[4 * q], w1[4 * q + 1], w1[4 * q + 2], w1[4 * q + 3]});
-#pragma unroll
-            for (int i = 0; i < NTC; ++i) {
-              part[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b0, part[0][i], 0, 0, 0);
-              part[1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b1, part[1][i], 0, 0, 0);
+            for (int q = 0; q < 4; ++q) {
+              uint32_t w0[4], w1[4];
+              decode_folded4<KIND>(f[0], h, g, q, w0, tab);
+              decode_folded4<KIND>(f[1], h, g, q, w1, tab);
+              if (q + 1 < 4) read_a(a8, h, q + 1);
+              mfma_group(a8[q], w0, w1);
             }
+          } else {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) read_a(a8, h, q);
+            uint32_t w0[16], w1[16];
+            decode_folded<KIND>(f[0], h, g, w0, tab);
+            decode_folded<KIND>(f[1], h, g, w1, tab);
+#pragma unroll
+            for (int q = 2; q < 4; ++q) read_a(a8, h, q);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) mfma_group(a8[q], w0 + 4 * q, w1 + 4 * q);
           }
         }
         const float s0 = step_scale<KIND>(f[0]), s1 = step_scale<KIND>(f[1]);
@@ -542,7 +596,7 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
   constexpr bool kStagedHere = STAGED && kStagedKind<KIND>;
   __shared__ __attribute__((aligned(16))) uint8_t w_lds[kStagedHere ? WAVES * 2 * kGroupBytes : 16];
   __shared__ DirectTables<KIND> tab;
-  __shared__ __attribute__((aligned(16))) f16 a_lds[(kStagedHere ? 2 : 1) * NT * 16 * kPitch];
+  __shared__ __attribute__((aligned(16))) f16 a_lds[(kStagedHere ? activation_buffers<NT>() : 1) * NT * 16 * kPitch];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -556,12 +610,23 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
   if (t0 >= p.n_tiles) return;
   const uint32_t e = p.tile_expert[t0];
   if (e >= (uint64_t)p.experts) return;  // a tile nothing fills: left out
-  if (t0 % NT != 0 && p.tile_expert[t0 - 1] == e) return;  // a tile of a chunk that starts before it
-  const int wend = min((t0 / NT + 1) * NT, p.n_tiles);
+  // A run of one expert's consecutive tiles is cut into chunks of NT from its first tile: this workgroup works if
+  // the run's tiles before t0 are a multiple of NT. Lane l looks at tile t0 - 1 - before - l.
+  int before = 0;
+  for (;;) {
+    const int t = t0 - 1 - before - (tid & 63);
+    const uint64_t other = __ballot(t < 0 || p.tile_expert[t] != e);
+    if (other != 0) {
+      before += __builtin_ctzll(other);
+      break;
+    }
+    before += 64;
+  }
+  if (__builtin_amdgcn_readfirstlane(before) % NT != 0) return;  // a tile of a chunk that starts before it
   int nt = 1;
 #pragma unroll
   for (int i = 1; i < NT; ++i)
-    if (t0 + i < wend && nt == i && p.tile_expert[t0 + i] == e) nt = i + 1;
+    if (t0 + i < p.n_tiles && nt == i && p.tile_expert[t0 + i] == e) nt = i + 1;
   nt = __builtin_amdgcn_readfirstlane(nt);
 
   {  // the codebooks, read after the K loop's first barrier
@@ -569,17 +634,21 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
     strata_mv::fetch_tables<KIND, kThreadsWg>(tf, tid);
     strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
   }
-  static_assert(NT == 2, "chunks of one or two tiles");
+  static_assert(NT == 2 || NT == 3, "chunks of up to two or three tiles");
   if constexpr (kStagedHere) {
     if (nt == 1)
       run_chunk_staged<KIND, MODE, OT, WAVES, NT, 1>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
-    else
+    else if (nt == 2)
       run_chunk_staged<KIND, MODE, OT, WAVES, NT, 2>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
+    else if constexpr (NT == 3)
+      run_chunk_staged<KIND, MODE, OT, WAVES, NT, 3>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
   } else {
     if (nt == 1)
       run_chunk<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, e, t0, rb, tid, wave);
-    else
+    else if (nt == 2)
       run_chunk<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, e, t0, rb, tid, wave);
+    else if constexpr (NT == 3)
+      run_chunk<KIND, MODE, OT, WAVES, 3>(p, tab, a_lds, e, t0, rb, tid, wave);
   }
 }
 
@@ -594,7 +663,7 @@ inline bool prompt_takes(int kind, int64_t cols) {
 }
 
 constexpr int kWaves = 4;
-constexpr int kTiles = 2;
+constexpr int kTiles = 3;  // tiles a chunk at most (an expert's rows decoded once for them)
 constexpr bool kStaged = true;  // rows through LDS by direct loads (run_chunk_staged)
 
 template <int KIND, int MODE, typename OT>
