@@ -13,7 +13,10 @@
 // Order of the loads. The codebook and the token are asked for first and the workgroup barrier waits for them
 // alone; the rows go out after it. A CU's loads return in the order they were asked for, so rows asked for
 // before the barrier put every wave's codebook load behind the other waves' rows: the barrier then passed at
-// 3.4-9 us into the launch instead of about 1 us (per-wave timestamps), and nothing was decoded until then.
+// 3.4-9 us into the launch instead of about 1 us (per-wave timestamps), and nothing was decoded until then. With a
+// barrier that waits for nothing once every wave has asked for its table entry and token (so that all of those
+// come before any row), the rows before the table still made the one-token gate/up launch slower, 17.0 against
+// 14.0 us.
 // For the same reason nothing of the decode may be moved above the barrier (opaque(): the compiler would
 // otherwise compute the codebook addresses there and wait for the rows at the barrier).
 //
