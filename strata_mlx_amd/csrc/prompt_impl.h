@@ -278,33 +278,45 @@ __device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTab
         f32x4 part[2][NTC];
 #pragma unroll
         for (int i = 0; i < NTC; ++i) part[0][i] = part[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto read_a = [&](f16x8 (&a8)[4][NTC], int h, int q) {
+#pragma unroll
+          for (int i = 0; i < NTC; ++i)
+            a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
+        };
+        auto mfma_group = [&](const f16x8 (&a8)[NTC], const uint32_t* w0, const uint32_t* w1) {
+          const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[0], w0[1], w0[2], w0[3]});
+          const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[0], w1[1], w1[2], w1[3]});
+#pragma unroll
+          for (int i = 0; i < NTC; ++i) {
+            f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
+            f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
+            p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[i], b0, p0, 0, 0, 0);
+            p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[i], b1, p1, 0, 0, 0);
+          }
+        };
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          f16x8 a8[4][NTC];  // the first two read ahead of the decode, so their latency passes under it
+          f16x8 a8[4][NTC];
+          if constexpr (NTC >= 3 && (KIND == K_IQ3_S || KIND == K_IQ3_XXS)) {  // a group pair at a time, as staged
+            read_a(a8, h, 0);
 #pragma unroll
-          for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int i = 0; i < NTC; ++i)
-              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
-          uint32_t w0[16], w1[16];
-          decode_folded<KIND>(f[sp][0], h, g, w0, tab);
-          decode_folded<KIND>(f[sp][1], h, g, w1, tab);
-#pragma unroll
-          for (int q = 2; q < 4; ++q)
-#pragma unroll
-            for (int i = 0; i < NTC; ++i)
-              a8[q][i] = *reinterpret_cast<const f16x8*>(a_lds + (i * 16 + n) * kPitch + a_col<KIND>(g, h, q));
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{w0[4 * q], w0[4 * q + 1], w0[4 * q + 2], w0[4 * q + 3]});
-            const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{w1[4 * q], w1[4 * q + 1], w1[4 * q + 2], w1[4 * q + 3]});
-#pragma unroll
-            for (int i = 0; i < NTC; ++i) {
-              f32x4& p0 = has_step_scale<KIND>() ? part[0][i] : acc[0][i];
-              f32x4& p1 = has_step_scale<KIND>() ? part[1][i] : acc[1][i];
-              p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b0, p0, 0, 0, 0);
-              p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8[q][i], b1, p1, 0, 0, 0);
+            for (int q = 0; q < 4; ++q) {
+              uint32_t w0[4], w1[4];
+              decode_folded4<KIND>(f[sp][0], h, g, q, w0, tab);
+              decode_folded4<KIND>(f[sp][1], h, g, q, w1, tab);
+              if (q + 1 < 4) read_a(a8, h, q + 1);
+              mfma_group(a8[q], w0, w1);
             }
+          } else {  // the first two groups' activations read ahead of the decode, so their latency passes under it
+#pragma unroll
+            for (int q = 0; q < 2; ++q) read_a(a8, h, q);
+            uint32_t w0[16], w1[16];
+            decode_folded<KIND>(f[sp][0], h, g, w0, tab);
+            decode_folded<KIND>(f[sp][1], h, g, w1, tab);
+#pragma unroll
+            for (int q = 2; q < 4; ++q) read_a(a8, h, q);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) mfma_group(a8[q], w0 + 4 * q, w1 + 4 * q);
           }
         }
         if constexpr (has_step_scale<KIND>()) {

@@ -59,12 +59,14 @@ def test_the_tile_product_is_the_product_with_the_weights(gpu, kind, dtype):
 
 
 @pytest.mark.parametrize("kind", ["IQ3_XXS", "IQ3_S", "Q2_0"])
-def test_runs_of_an_experts_tiles_of_any_length(gpu, kind):
+@pytest.mark.parametrize("cols", [512, 256])
+def test_runs_of_an_experts_tiles_of_any_length(gpu, kind, cols):
     """The prompt kernels cut each run of one expert's consecutive tiles into chunks from the run's first tile:
     runs of 1 to 7 tiles, one of 70 (past the 64 tiles a look back covers at once), the same expert again after
-    others, and tiles of no expert between them; every tile's product against the oracle's weights."""
+    others, and tiles of no expert between them; every tile's product against the oracle's weights. Rows of 256
+    columns (98 or 110 bytes, not whole dwords) take the kernels that load the fields straight into registers."""
     rng = np.random.default_rng(11)
-    shape = (4, 64, 512)
+    shape = (4, 64, cols)
     data, w = stack(kind, rng, *shape)
     w = w.astype(np.float32).astype(np.float64)  # exact for these types at whole blocks (see above)
     runs = [(2, 1), (0, 2), (1, 3), (4, 1), (3, 4), (2, 5), (0, 7), (1, 70), (0, 1), (4, 2), (3, 2), (0, 6)]
