@@ -226,7 +226,7 @@ def prompt_check(gpu, layer, kind, tokens, dtype, seed, x_scale=1.0):
     h = silu.astype(np.float32)
     h = torch.from_numpy(h).to(dtype).float().numpy() if dtype == torch.bfloat16 else h.astype(npdt)
     want = as_dtype(down_oracle(layer, h, sub), dtype)
-    assert counts[by[-1]] > 16 * 8  # the heaviest expert fills several windows of tiles
+    assert counts[by[-1]] > 16 * 8  # the heaviest expert fills several chunks of tiles
     assert rel_l2(y[pairs], want) <= REL, sorted(sample)
 
 
