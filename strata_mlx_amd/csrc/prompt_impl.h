@@ -623,16 +623,31 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
   const uint32_t e = p.tile_expert[t0];
   if (e >= (uint64_t)p.experts) return;  // a tile nothing fills: left out
   // A run of one expert's consecutive tiles is cut into chunks of NT from its first tile: this workgroup works if
-  // the run's tiles before t0 are a multiple of NT. Lane l looks at tile t0 - 1 - before - l.
-  int before = 0;
-  for (;;) {
-    const int t = t0 - 1 - before - (tid & 63);
-    const uint64_t other = __ballot(t < 0 || p.tile_expert[t] != e);
-    if (other != 0) {
-      before += __builtin_ctzll(other);
-      break;
+  // the run's tiles before t0 are a multiple of NT. The first round looks at the 64 tiles before t0 (lane l at
+  // t0 - 1 - l), which settles every run of up to 64 tiles; each later one at the next 256 (lane l at
+  // t0 - 1 - before - 64 j - l, j = 0..3, four loads in flight at once), so that a run of thousands of tiles takes
+  // a few rounds. (Four loads from the first round on cost 1 % at the usual routings.)
+  int before;
+  {
+    const int t = t0 - 1 - (tid & 63);
+    const uint64_t m = __ballot(t < 0 || p.tile_expert[t] != e);
+    before = m != 0 ? __builtin_ctzll(m) : 64;
+  }
+  for (bool more = before == 64; more;) {
+    bool other[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = t0 - 1 - before - 64 * j - (tid & 63);
+      other[j] = t < 0 || p.tile_expert[t] != e;
     }
-    before += 64;
+    int seen = 256;  // tiles of the run among those looked at, before the first other one
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      const uint64_t m = __ballot(other[j]);
+      if (m != 0) seen = 64 * j + __builtin_ctzll(m);
+    }
+    before += seen;
+    more = seen == 256;
   }
   if (__builtin_amdgcn_readfirstlane(before) % NT != 0) return;  // a tile of a chunk that starts before it
   int nt = 1;

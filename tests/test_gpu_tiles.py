@@ -62,14 +62,15 @@ def test_the_tile_product_is_the_product_with_the_weights(gpu, kind, dtype):
 @pytest.mark.parametrize("cols", [512, 256])
 def test_runs_of_an_experts_tiles_of_any_length(gpu, kind, cols):
     """The prompt kernels cut each run of one expert's consecutive tiles into chunks from the run's first tile:
-    runs of 1 to 7 tiles, one of 70 (past the 64 tiles a look back covers at once), the same expert again after
-    others, and tiles of no expert between them; every tile's product against the oracle's weights. Rows of 256
+    runs of 1 to 7 tiles, of 70 and of 300 (past the 256 tiles a look back covers at once), the same expert again
+    after others, and tiles of no expert between them; every tile's product against the oracle's weights. Rows of 256
     columns (98 or 110 bytes, not whole dwords) take the kernels that load the fields straight into registers."""
     rng = np.random.default_rng(11)
     shape = (4, 64, cols)
     data, w = stack(kind, rng, *shape)
     w = w.astype(np.float32).astype(np.float64)  # exact for these types at whole blocks (see above)
-    runs = [(2, 1), (0, 2), (1, 3), (4, 1), (3, 4), (2, 5), (0, 7), (1, 70), (0, 1), (4, 2), (3, 2), (0, 6)]
+    runs = [(2, 1), (0, 2), (1, 3), (4, 1), (3, 4), (2, 5), (0, 7), (1, 70), (0, 1), (4, 2), (3, 2), (0, 6), (2, 300),
+            (3, 1)]
     tiles = np.concatenate([np.full(n, e) for e, n in runs])  # expert 4: no expert, left out
     a = torch.from_numpy(rng.standard_normal((16 * len(tiles), shape[2])).astype(np.float16))
     got = B.tile_matmul(dev(data, gpu), kind, shape, a.to(gpu), dev(tiles.astype(np.int32), gpu)).cpu().numpy()
