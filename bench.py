@@ -2,13 +2,15 @@
 """Benchmark of the expert dequant-matmul path on one MI355X.
 
 Headline (value): routed-expert decode matvec, IQ3_S, 256 experts top-8 of Zipf(1.1) routing, gate/up 1536 x 4096
-and down 4096 x 1536, the SwiGLU in gate/up's launch, float16 activations, batch 1. A step is one decode pass of the
-batch through 16 distinct routed-expert layers (about 1 GB of expert bytes, four times the 256 MB MALL), captured
-once as a HIP graph and replayed; each layer is two launches (gate+up writing silu(gate) * up, then down).
-value = algorithmic bytes / time: the distinct experts' packed bytes plus activations in and out.
+and down 4096 x 1536 with the SwiGLU between them, float16 activations, batch 1. A step is one decode pass of the
+batch through 16 distinct routed-expert layers (about 1 GB of expert bytes, four times the 256 MB MALL), each a
+BlockSwitchGLU call as the engine makes it, captured once as a HIP graph and replayed; at one token a layer is one
+launch (gate, up, SwiGLU and down: strata_expert_layer). value = algorithmic bytes / time: the distinct experts'
+packed bytes plus activations in and out (x, h written and read, y). two_launches: the same layers as the
+gate+up+SwiGLU launch followed by the down launch.
 
 Beside it, on the same line, the other workloads of the path:
-  decode_t4      the same at 4 tokens
+  decode_t4      the same at 4 tokens (two launches a layer)
   speculate      the same layer in Q2_0, 5 rows (1 + 4 draft tokens), 16 layers
   q4k_matvec     one Q4_K 4096 x 4096 matrix, float32 x, batch 1 (graphs of 64 distinct copies), and its CPU path
   prompt         512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, the fused
@@ -20,8 +22,8 @@ Beside it, on the same line, the other workloads of the path:
                  routed gate+up launches instead (its marginal time over those launches alone)
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
                  the dense layers dequantized for the chunk and multiplied by the library product, TFLOPS
-  roofline       the dominant kernel (gate+up+SwiGLU matvec): algorithmic bytes per launch / its mean duration
-                 (HIP events around a graph of those launches only), against 8 TB/s
+  roofline       the dominant kernel (the one-launch layer): algorithmic bytes per launch / its mean duration
+                 (HIP events around the graph of those launches, on the stream they run on), against 8 TB/s
   cpu_baseline   the oracle's numpy decode of the touched experts (one thread) + float32 matvecs (BLAS on the
                  host's cores) on a few layers of the headline workload; q4k_matvec carries its own
 
@@ -103,38 +105,49 @@ def decode_layers(B, synth, dev, layers, kind="IQ3_S", seed=0):
 
 
 def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
-    """Returns (GB/s, ms per step, bytes per step, gate/up launch: (bytes, mean seconds), routes)."""
+    """A step: every layer of `lins` called as the engine calls it (BlockSwitchGLU: the gate/up/SwiGLU launch, then
+    down). Returns (GB/s, ms per step, bytes per step, (mean bytes of a layer, mean seconds of a layer), routes, GB/s
+    of the same layers as one launch each (strata_expert_layer; None where it does not take the case))."""
     routes = [synth.zipf_routing(tokens, E, K, rng)[0] for _ in lins]
     idx = [torch.from_numpy(r).to(torch.int32).to(dev) for r in routes]
     x = (torch.randn((tokens, H), device=dev)).half()
     mat_bytes = lins[0][0].blocks.numel() // E
+    glus = [B.BlockSwitchGLU(gate, up, down) for gate, up, down in lins]
+
+    def layered():
+        for glu, ix in zip(glus, idx):
+            glu(x, ix)
+
+    def one_launch():
+        for (gate, up, down), ix in zip(lins, idx):
+            B.expert_layer(gate, up, down, x, ix.reshape(-1))
+
+    one = tokens == 1
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
+    graphs = {}
     with torch.cuda.stream(stream):  # one eager pass first: the library's lazy state, torch's allocator
-        for (gate, up, down), ix in zip(lins, idx):
-            h = B.gate_up_swiglu(gate, up, x, ix, K)[2]
-            B.expert_matvec(down, ix.reshape(-1), h)
+        for name, run in (("layer", layered), ("one", one_launch))[:2 if one else 1]:
+            run()
+            torch.cuda.synchronize()
+            graphs[name] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[name], stream=stream):
+                run()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    full, gu = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-    with torch.cuda.graph(full):
-        for (gate, up, down), ix in zip(lins, idx):
-            h = B.gate_up_swiglu(gate, up, x, ix, K)[2]
-            B.expert_matvec(down, ix.reshape(-1), h)
-    with torch.cuda.graph(gu):
-        for (gate, up, down), ix in zip(lins, idx):
-            B.gate_up_swiglu(gate, up, x, ix, K)
-    step_bytes, gu_bytes = 0, 0
+    step_bytes = 0
     for r in routes:
         d = len(np.unique(r))
-        act = tokens * H * 2 + tokens * K * F * 2  # x in; silu(gate) * up out (gate and up themselves not counted)
-        gu_bytes += d * 2 * mat_bytes + act
-        step_bytes += d * 3 * mat_bytes + act + tokens * K * F * 2 + tokens * K * H * 2  # down: h in, y out
-    t = time_graph(full, steps, warmup)
-    t_gu = time_graph(gu, steps, warmup)
-    launches = steps * len(lins)
-    return (step_bytes * steps / t / 1e9, t / steps * 1e3, step_bytes, (gu_bytes / len(lins), t_gu / launches),
-            routes)
+        # the distinct experts' gate, up and down; x in, h between the halves (written and read), y out
+        step_bytes += d * 3 * mat_bytes + tokens * H * 2 + 2 * tokens * K * F * 2 + tokens * K * H * 2
+    t = time_graph(graphs["layer"], steps, warmup)
+    gbs_one = None
+    if one:
+        gbs_one = step_bytes * steps / time_graph(graphs["one"], steps, warmup) / 1e9
+        if B.layer_status(dev):
+            raise RuntimeError("a wait of the one-launch layer gave up")
+    layer = (step_bytes / len(lins), t / steps / len(lins))
+    return step_bytes * steps / t / 1e9, t / steps * 1e3, step_bytes, layer, routes, gbs_one
 
 
 def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512):
@@ -431,34 +444,43 @@ def main():
     note(f"making {args.layers} IQ3_S layers of 256 experts")
     lins = decode_layers(B, synth, dev, args.layers)
     note("decode, batch {}".format(args.tokens))
-    gbs, ms, step_bytes, (gu_bytes, gu_s), routes = decode_bench(B, synth, dev, lins, args.tokens, args.steps,
-                                                                 args.warmup, rng)
-    note(f"decode: {gbs:.1f} GB/s; batch 4")
-    gbs4, ms4, _, (gu4_bytes, gu4_s), _ = decode_bench(B, synth, dev, lins, 4, args.steps, args.warmup, rng)
-    achieved = gu_bytes / gu_s / 1e9
+    gbs, ms, step_bytes, (lay_bytes, lay_s), routes, gbs_one = decode_bench(B, synth, dev, lins, args.tokens,
+                                                                             args.steps, args.warmup, rng)
+    note(f"decode: {gbs:.1f} GB/s (one launch a layer: {gbs_one}); batch 4")
+    gbs4, ms4, _, _, _, _ = decode_bench(B, synth, dev, lins, 4, args.steps, args.warmup, rng)
+    achieved = lay_bytes / lay_s / 1e9
+    one = args.tokens == 1
     result = {
         "metric": "expert decode matvec GB/s (% HBM peak) + prompt dequant-GEMM TFLOPS",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16", "data": "synthetic (random IQ3_S blocks, d=|N(0,1)|*0.01; Zipf(1.1) top-8 routing)",
+        "dtype": "f16",
+        "data": "synthetic: random IQ3_S blocks (d=|N(0,1)|*0.01), Zipf(1.1) top-8 routing, x ~ N(0,1) float16 as the "
+                "workload names it; on these random blocks the float16 SwiGLU and down overflow to inf in part, which "
+                "no launch's timing depends on (the parity tests run the same launches at x ~ N(0,1)/64)",
         "config": {"workload": f"routed-expert decode, IQ3_S, 256 experts top-8, gate/up 1536x4096, down 4096x1536, "
-                               f"SwiGLU in gate/up, batch {args.tokens}; a step = {args.layers} distinct layers",
+                               f"SwiGLU, batch {args.tokens}; a step = {args.layers} distinct layers, each one "
+                               f"BlockSwitchGLU call" + (" (one launch)" if one else ""),
                    "tokens": args.tokens, "experts": E, "top_k": K, "hidden": H, "ffn": F, "layers": args.layers,
                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "one_launch": None if gbs_one is None else {
+            "gbs": round(gbs_one, 1), "hbm_frac": round(gbs_one / HBM_PEAK_GBS, 4),
+            "note": "the same layers as one launch each (routed_layer_kernel: gate, up, SwiGLU and down, the pair's "
+                    "h handed over in memory; strata_expert_layer)"},
         "decode_t4": {"gbs": round(gbs4, 1), "ms_per_step": round(ms4, 4), "hbm_frac": round(gbs4 / HBM_PEAK_GBS, 4),
-                      "gate_up_kernel_gbs": round(gu4_bytes / gu4_s / 1e9, 1)},
+                      "note": "gate/up/SwiGLU then down, two launches a layer"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "routed_glu_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
-                     "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
+                     "kernel": ("routed_layer_kernel IQ3_S: gate, up, SwiGLU and down of one token, one launch a "
+                                "layer (strata_expert_layer)") if one else "the layer's two launches",
+                     "bytes_per_launch": int(lay_bytes), "mean_launch_us": round(lay_s * 1e6, 3)},
     }
     if not args.no_extra:
         note("speculative verify, Q2_0, 5 rows")
         q2 = decode_layers(B, synth, dev, args.layers, "Q2_0", seed=7)
-        gq, msq, _, (gq_bytes, gq_s), _ = decode_bench(B, synth, dev, q2, 5, args.steps, args.warmup, rng)
+        gq, msq, _, _, _, _ = decode_bench(B, synth, dev, q2, 5, args.steps, args.warmup, rng)
         result["speculate"] = {"workload": "Q2_0 routed decode, 256 experts top-8, 5 rows (1 + 4 draft), 16 layers",
-                               "gbs": round(gq, 1), "ms_per_step": round(msq, 4), "hbm_frac": round(gq / HBM_PEAK_GBS, 4),
-                               "gate_up_kernel_gbs": round(gq_bytes / gq_s / 1e9, 1)}
+                               "gbs": round(gq, 1), "ms_per_step": round(msq, 4), "hbm_frac": round(gq / HBM_PEAK_GBS, 4)}
         del q2
         torch.cuda.empty_cache()
         note("Q4_K 4096 x 4096, float32 x")

@@ -85,6 +85,24 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
                                         int shared_kind, const void* shared_gate, const void* shared_up,
                                         int64_t shared_rows, void* shared_h, void* stream);
 
+/* The routed experts of one decode token in one launch: h[p, :] = swiglu(gate[idx[p]] . x, up[idx[p]] . x) rounded
+ * as strata_expert_gate_up_swiglu rounds it, then out[p, :] = down[idx[p]] . h[p, :]; the same bits as those two
+ * calls (strata_expert_gate_up_swiglu, then strata_expert_matvec on down). gate, up (experts, ffn, hidden) and down
+ * (experts, hidden, ffn) stacks of `kind` IQ3_S or Q2_0, hidden 4096, ffn 1536 or 2560; x one float16 token;
+ * pairs 1 to 16; out (pairs, hidden) float16; out_h (pairs, ffn) float16 or NULL. A pair naming no expert gets
+ * NaN rows. `workspace`: device memory of strata_expert_layer_workspace(pairs, ffn) bytes, zeroed before its first
+ * call and then given to every call of that shape on one device and one stream (calls that share a workspace
+ * must not overlap). One workgroup a CU runs for the launch and the workgroups of a pair wait for each other's h:
+ * each wait gives up after `spin` polls of memory (about a microsecond each; 100000 is ample), writes NaN to its
+ * rows of out and sets bit 0 of the workspace's first uint32, which the caller reads and clears. Replaces the
+ * per-pair path of switch_glu at one token, strata_mlx/blocks.py:958-986 (the gate and up calls, then matvec_glu's
+ * down with the SwiGLU, :939-955). */
+int64_t strata_expert_layer_workspace(int64_t pairs, int64_t ffn);
+int strata_expert_layer(int kind, const void* gate_blocks, const void* up_blocks, const void* down_blocks,
+                        int64_t experts, int64_t hidden, int64_t ffn, const uint32_t* idx, int64_t pairs,
+                        const void* x, int x_dtype, void* out_h, void* out, void* workspace, int64_t spin,
+                        void* stream);
+
 /* out[p, r] = W[idx[p], r, :] . swiglu(gate[p], up[p]) with the SwiGLU rounded as mlx-lm rounds it
  * (sigmoid in float32 rounded to the activation dtype, then two products in that dtype); gate, up
  * (pairs, cols). Replaces matvec_glu + _MATVEC_GLU, strata_mlx/blocks.py:939-955, 225-259. */

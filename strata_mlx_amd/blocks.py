@@ -178,6 +178,69 @@ def gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: tor
     return g, u, h, sh
 
 
+LAYER_SPIN = 100000  # polls of memory (about a microsecond each) before a wait of expert_layer gives up
+_layer_workspaces = {}
+
+
+def _layer_workspace(device: torch.device, pairs: int, ffn: int) -> torch.Tensor:
+    """The workspace of expert_layer for one device, stream and shape, zeroed when first made and kept."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream, pairs, ffn)
+    ws = _layer_workspaces.get(key)
+    if ws is None:
+        size = _lib.library().strata_expert_layer_workspace(pairs, ffn)
+        if size < 0:
+            raise ValueError(f"expert_layer: {pairs} pairs of {ffn} rows not taken")
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _layer_workspaces[key] = ws
+    return ws
+
+
+def layer_status(device: torch.device | None = None) -> int:
+    """The status bits that expert_layer's launches on `device` set since the last call (bit 0: a wait gave up and
+    wrote NaN rows), cleared on return. Waits for the device."""
+    status = 0
+    for (index, _, _, _), ws in _layer_workspaces.items():
+        if device is None or index == torch.device(device).index:
+            word = ws[:4].view(torch.int32)
+            status |= int(word.item())
+            word.zero_()
+    return status
+
+
+def expert_layer(gate: BlockSwitchLinear, up: BlockSwitchLinear, down: BlockSwitchLinear, x: torch.Tensor,
+                 idx: torch.Tensor, with_h: bool = False):
+    """down(silu(gate . x) * (up . x)) for every pair of one token, in one launch: x (1, in) float16, idx (pairs,)
+    -> (pairs, out), or (y, h) with h (pairs, ffn) if with_h. The same bits as gate_up_swiglu followed by
+    expert_matvec on down. None where the launch does not take the case (other types or shapes, several tokens):
+    the caller then makes those two calls. The per-pair path of strata_mlx/blocks.py:958-986 at one token."""
+    if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) != (up.kind, up.output_dims, up.input_dims,
+                                                                             up.num_experts):
+        raise ValueError("gate and up differ in type or shape")
+    if (down.kind, down.num_experts, down.input_dims, down.output_dims) != (gate.kind, gate.num_experts,
+                                                                             gate.output_dims, gate.input_dims):
+        return None
+    x2 = x.reshape(-1, gate.input_dims)
+    pairs = idx.numel()
+    if x2.shape[0] != 1 or x.dtype != torch.float16 or not 1 <= pairs <= 16:
+        return None
+    x2 = x2.contiguous()
+    lib = _lib.library()
+    if lib.strata_expert_layer_workspace(pairs, gate.output_dims) < 0:
+        return None
+    ws = _layer_workspace(x.device, pairs, gate.output_dims)
+    y = torch.empty((pairs, down.output_dims), dtype=x.dtype, device=x.device)
+    h = torch.empty((pairs, gate.output_dims), dtype=x.dtype, device=x.device) if with_h else None
+    idx = _idx32(idx)
+    rc = lib.strata_expert_layer(
+        _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), down.blocks.data_ptr(),
+        gate.num_experts, gate.input_dims, gate.output_dims, idx.data_ptr(), pairs, x2.data_ptr(),
+        _lib.dtype_id(x.dtype), _lib.ptr(h), y.data_ptr(), ws.data_ptr(), LAYER_SPIN, _lib.stream())
+    if rc in (_lib.ERR_KIND, _lib.ERR_SHAPE):
+        return None
+    _lib.check(rc, f"expert layer {gate.kind}")
+    return (y, h) if with_h else y
+
+
 def expert_matvec(lin: BlockSwitchLinear, idx: torch.Tensor, x: torch.Tensor, share: int = 1) -> torch.Tensor:
     """out[pair] = W[idx[pair]] . x[pair / share]: x (pairs / share, in) -> (pairs, out)."""
     pairs = idx.numel()
