@@ -74,7 +74,8 @@ int strata_expert_gate_up_swiglu(int kind, const void* gate_blocks, const void* 
 
 /* strata_expert_gate_up_swiglu at one token (every pair reads x's one row) with a shared expert's gate and up
  * in the same launch: shared_h[r] = silu(shared_gate[r, :] . x) * (shared_up[r, :] . x), rounded as out_h;
- * shared_gate, shared_up (shared_rows, cols). The routed stacks IQ3_S or Q2_0 of 4096 inputs, x float16, the
+ * shared_gate, shared_up (shared_rows, cols); shared_g and shared_u (each NULL or (shared_rows,)) get the shared
+ * expert's gate . x and up . x as float16. The routed stacks IQ3_S or Q2_0 of 4096 inputs, x float16, the
  * shared expert Q4_K; other cases return STRATA_ERR_SHAPE, and the caller makes the two calls apart. No single
  * counterpart in the reference, whose MoE block calls the routed experts and then the shared expert
  * (strata_mlx/fused.py:492-493, the gate and up of each, with the SwiGLU of their down calls): the routed
@@ -83,7 +84,8 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
                                         int64_t rows, int64_t cols, const uint32_t* idx, int64_t pairs,
                                         const void* x, int x_dtype, void* out_gate, void* out_up, void* out_h,
                                         int shared_kind, const void* shared_gate, const void* shared_up,
-                                        int64_t shared_rows, void* shared_h, void* stream);
+                                        int64_t shared_rows, void* shared_h, void* shared_g, void* shared_u,
+                                        void* stream);
 
 /* The routed experts of one decode token in one launch: h[p, :] = swiglu(gate[idx[p]] . x, up[idx[p]] . x) rounded
  * as strata_expert_gate_up_swiglu rounds it, then out[p, :] = down[idx[p]] . h[p, :]; the same bits as those two

@@ -144,12 +144,13 @@ def gate_up_swiglu(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tens
 
 
 def gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tensor, idx: torch.Tensor,
-                          shared_gate, shared_up):
+                          shared_gate, shared_up, with_shared_gu: bool = False):
     """gate_up_swiglu at one token with a shared expert's gate and up (layers of the file's Q4_K blocks with
     `blocks`, `kind`, `output_dims`, `input_dims`: dense.BlockLinear) in the same launch: (g, u, h) of the pairs
-    and the shared expert's h (1, shared rows). None where the launch does not take the case (other types, several
-    tokens, inputs other than 4096): the caller then makes the two calls apart. The routed experts' and the shared
-    expert's gate and up of strata_mlx/fused.py:492-493, with the SwiGLU of their down calls."""
+    and the shared expert's h (1, shared rows), and its own gate . x and up . x (1, shared rows) after those if
+    with_shared_gu. None where the launch does not take the case (other types, several tokens, inputs other than
+    4096): the caller then makes the two calls apart. The routed experts' and the shared expert's gate and up of
+    strata_mlx/fused.py:492-493, with the SwiGLU of their down calls."""
     if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) != (up.kind, up.output_dims, up.input_dims,
                                                                              up.num_experts):
         raise ValueError("gate and up differ in type or shape")
@@ -166,16 +167,17 @@ def gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: tor
     g = torch.empty((pairs, gate.output_dims), dtype=x.dtype, device=x.device)
     u, h = torch.empty_like(g), torch.empty_like(g)
     sh = torch.empty((1, shared_gate.output_dims), dtype=x.dtype, device=x.device)
+    sgu = (torch.empty_like(sh), torch.empty_like(sh)) if with_shared_gu else (None, None)
     idx = _idx32(idx)
     rc = _lib.library().strata_expert_gate_up_swiglu_shared(
         _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), gate.num_experts, gate.output_dims,
         gate.input_dims, idx.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), g.data_ptr(), u.data_ptr(),
         h.data_ptr(), _lib.kind_id(shared_gate.kind), shared_gate.blocks.data_ptr(), shared_up.blocks.data_ptr(),
-        shared_gate.output_dims, sh.data_ptr(), _lib.stream())
+        shared_gate.output_dims, sh.data_ptr(), _lib.ptr(sgu[0]), _lib.ptr(sgu[1]), _lib.stream())
     if rc in (_lib.ERR_SHAPE, _lib.ERR_DTYPE):
         return None
     _lib.check(rc, f"gate/up/swiglu with the shared expert {gate.kind} + {shared_gate.kind}")
-    return g, u, h, sh
+    return (g, u, h, sh, *sgu) if with_shared_gu else (g, u, h, sh)
 
 
 LAYER_SPIN = 100000  # polls of memory (about a microsecond each) before a wait of expert_layer gives up

@@ -12,9 +12,10 @@
 namespace strata_gemm {
 
 int STRATA_CAT(gemm_launch_, STRATA_KIND)(GemmParams& p, int a_dtype, hipStream_t s) {
-  // IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight steps with float16 activations: the register-decode kernel
+  // IQ3_S / IQ3_XXS / Q2_0 rows of whole 256-weight steps with float16 activations: the register-decode kernel,
+  // whose row offsets within a matrix are 32-bit (larger matrices take the other kernel)
   if constexpr (strata_mv::FastTraits<STRATA_KIND>::supported) {
-    if (a_dtype == DT_F16 && strata_prompt::prompt_takes(STRATA_KIND, p.cols)) {
+    if (a_dtype == DT_F16 && strata_prompt::prompt_takes(STRATA_KIND, p.cols) && p.mat_bytes < (int64_t(1) << 32)) {
       strata_prompt::PromptParams q = {};
       q.blocks[0] = p.blocks;
       q.a = reinterpret_cast<const f16*>(p.a);

@@ -144,7 +144,7 @@ int expert_common(int kind, const void* a, const void* b, int64_t experts, int64
 
 extern "C" {
 
-int strata_abi_version(void) { return 2; }
+int strata_abi_version(void) { return 3; }
 
 int strata_block_info(int kind, int* per_block, int* block_bytes) {
   return strata_kind_info(kind, per_block, block_bytes) ? STRATA_ERR_KIND : STRATA_OK;
@@ -192,7 +192,8 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
                                         int64_t rows, int64_t cols, const uint32_t* idx, int64_t pairs,
                                         const void* x, int x_dtype, void* out_gate, void* out_up, void* out_h,
                                         int shared_kind, const void* shared_gate, const void* shared_up,
-                                        int64_t shared_rows, void* shared_h, void* stream) {
+                                        int64_t shared_rows, void* shared_h, void* shared_g, void* shared_u,
+                                        void* stream) {
   MatvecParams p = {};
   int rc = block_shape(kind, rows, cols, &p.row_bytes);
   if (rc) return rc;
@@ -223,6 +224,8 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
   p.shared[0] = (const uint8_t*)shared_gate;
   p.shared[1] = (const uint8_t*)shared_up;
   p.shared_out = shared_h;
+  p.shared_gu[0] = shared_g;
+  p.shared_gu[1] = shared_u;
   p.shared_rows = (int)shared_rows;
   p.shared_row_bytes = s_row_bytes;
   return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 2, (hipStream_t)stream);

@@ -48,6 +48,7 @@ struct MatvecParams {
   // a shared expert in the routed gate/up launch (one token): its Q4_K gate and up (shared_rows x cols) and its h
   const uint8_t* shared[2];
   void* shared_out;
+  void* shared_gu[2];  // the shared expert's gate . x and up . x, or null
   int shared_rows, shared_row_bytes;
 };
 

@@ -132,6 +132,9 @@ int common_checks(int kind, int64_t experts, int64_t rows, int64_t cols, int64_t
     return cols > 0 && cols % per == 0 ? STRATA_ERR_KIND : STRATA_ERR_SHAPE;
   }
   if (rows < 0 || rows > (1 << 24) || cols > (1 << 20)) return STRATA_ERR_SHAPE;
+  int per = 0, bb = 0;
+  strata_kind_info(kind, &per, &bb);
+  if (rows * (cols / per * bb) >= (int64_t(1) << 32)) return STRATA_ERR_SHAPE;  // row offsets in a matrix are 32-bit
   if (dtype != DT_F16 && dtype != DT_BF16) return STRATA_ERR_DTYPE;
   if (tile != 16 || n_tiles < 0 || n_tiles > (1 << 24) || experts < 0) return STRATA_ERR_ARG;
   return STRATA_OK;

@@ -661,21 +661,26 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
     strata_mv::fetch_tables<KIND, kThreadsWg>(tf, tid);
     strata_mv::store_tables<KIND, kThreadsWg>(tab, tf, tid);
   }
-  static_assert(NT == 2 || NT == 3, "chunks of up to two or three tiles");
-  if constexpr (kStagedHere) {
-    if (nt == 1)
-      run_chunk_staged<KIND, MODE, OT, WAVES, NT, 1>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
-    else if (nt == 2)
-      run_chunk_staged<KIND, MODE, OT, WAVES, NT, 2>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
-    else if constexpr (NT == 3)
-      run_chunk_staged<KIND, MODE, OT, WAVES, NT, 3>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
-  } else {
-    if (nt == 1)
-      run_chunk<KIND, MODE, OT, WAVES, 1>(p, tab, a_lds, e, t0, rb, tid, wave);
-    else if (nt == 2)
-      run_chunk<KIND, MODE, OT, WAVES, 2>(p, tab, a_lds, e, t0, rb, tid, wave);
-    else if constexpr (NT == 3)
-      run_chunk<KIND, MODE, OT, WAVES, 3>(p, tab, a_lds, e, t0, rb, tid, wave);
+  static_assert(NT >= 2 && NT <= 8, "chunks of up to two to eight tiles");
+  // the body compiled for each chunk size up to NT: no branch between the MFMAs
+  auto go = [&](auto ntc) {
+    constexpr int NTC = decltype(ntc)::value;
+    if constexpr (NTC <= NT) {
+      if constexpr (kStagedHere)
+        run_chunk_staged<KIND, MODE, OT, WAVES, NT, NTC>(p, tab, a_lds, w_lds, e, t0, rb, tid, wave);
+      else
+        run_chunk<KIND, MODE, OT, WAVES, NTC>(p, tab, a_lds, e, t0, rb, tid, wave);
+    }
+  };
+  switch (nt) {
+    case 1: go(std::integral_constant<int, 1>()); break;
+    case 2: go(std::integral_constant<int, 2>()); break;
+    case 3: go(std::integral_constant<int, 3>()); break;
+    case 4: go(std::integral_constant<int, 4>()); break;
+    case 5: go(std::integral_constant<int, 5>()); break;
+    case 6: go(std::integral_constant<int, 6>()); break;
+    case 7: go(std::integral_constant<int, 7>()); break;
+    default: go(std::integral_constant<int, 8>()); break;
   }
 }
 

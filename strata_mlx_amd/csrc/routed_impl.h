@@ -289,6 +289,8 @@ struct GluParams {
   const uint8_t* s_gate;
   const uint8_t* s_up;
   f16* s_h;
+  f16* s_g;  // the shared expert's gate . x, or null
+  f16* s_u;  // its up . x, or null
   int s_rows, s_row_bytes;
 };
 
@@ -574,6 +576,8 @@ __global__ __launch_bounds__((glu_threads<KIND, MODE>()), (glu_threads<KIND, MOD
       if (lane == 0) {
         const f16 gq = from_f32<f16>(g), uq = from_f32<f16>(u);
         p.s_h[s_unit] = from_f32<f16>(swiglu_rounded<f16>(gq, uq));
+        if (p.s_g != nullptr) p.s_g[s_unit] = gq;
+        if (p.s_u != nullptr) p.s_u[s_unit] = uq;
       }
     }
   }
@@ -813,6 +817,8 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
       p.s_gate = mp.shared[0];
       p.s_up = mp.shared[1];
       p.s_h = reinterpret_cast<f16*>(mp.shared_out);
+      p.s_g = reinterpret_cast<f16*>(mp.shared_gu[0]);
+      p.s_u = reinterpret_cast<f16*>(mp.shared_gu[1]);
       p.s_rows = mp.shared_rows;
       p.s_row_bytes = mp.shared_row_bytes;
       p.na = p.pairs;

@@ -193,6 +193,25 @@ def test_dense_decode_layers_of_the_mixed_model(gpu, kind, rows):
     assert rel_l2(got[pick], want) <= REL
 
 
+def test_fused_qkv_as_benchmarked(gpu):
+    """The decode benchmark's q/k/v: three Q6_K 4096 x 4096 layers fused into one 12288-row matrix (dense.FusedLinear,
+    one launch: the one-matrix form at three units a wave), one float16 token, against the oracle on 1024 rows of
+    each of q, k and v (the first and last rows included)."""
+    parts = [Stack("Q6_K", 1, 4096, 4096, 650 + i, gpu) for i in range(3)]
+    fused = D.FusedLinear([D.BlockLinear(p.blocks, "Q6_K", (4096, 4096)) for p in parts])
+    x = np.random.default_rng(12).standard_normal((1, 4096)).astype(np.float16)
+    xs = torch.from_numpy(x).to(gpu)
+    outs = fused(xs)
+    whole = B.window_matvec(fused.blocks, "Q6_K", 3 * 4096, 4096, xs)  # the benchmark's call
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat(outs, dim=-1), whole)
+    pick = np.sort(np.random.default_rng(13).choice(4096, 1024, replace=False))
+    pick[0], pick[-1] = 0, 4095
+    for part, got in zip(parts, outs):
+        want = part.weights(0, pick).astype(np.float64) @ x[0].astype(np.float64)
+        assert rel_l2(got.float().cpu().numpy()[0][pick], want) <= REL
+
+
 def prompt_check(gpu, layer, kind, tokens, dtype, seed, x_scale=1.0):
     """A prompt chunk through switch_glu's tiles, every pair of a sample of experts (the heaviest, a middling one,
     the lightest used, and those of a few random pairs) against the oracle's chain g, u -> SwiGLU rounded to the
@@ -235,6 +254,43 @@ def test_prompt_chunk_as_benchmarked(gpu):
     layer = {n: Stack("IQ3_XXS", E, r, c, 500 + i, gpu) for i, (n, (r, c)) in
              enumerate((("gate", (F, H)), ("up", (F, H)), ("down", (H, F))))}
     prompt_check(gpu, layer, "IQ3_XXS", 512, torch.bfloat16, 4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prompt_chunk_in_q2_0(gpu, dtype):
+    """Config 4's shape in Q2_0 (the prompt target of the north star names IQ3_S and Q2_0): 512 tokens, 256 experts
+    top-8 of Zipf routing, gate/up 1536 x 4096 and down 4096 x 1536, through switch_glu's tiles (the fused gate/up
+    SwiGLU and scatter-down kernels on Q2_0's unstaged field loads), bfloat16 and float16."""
+    layer = {n: Stack("Q2_0", E, r, c, 520 + i, gpu) for i, (n, (r, c)) in
+             enumerate((("gate", (F, H)), ("up", (F, H)), ("down", (H, F))))}
+    prompt_check(gpu, layer, "Q2_0", 512, dtype, 14)
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "IQ3_XXS", "Q2_0"])
+def test_prompt_rows_of_three_steps(gpu, kind):
+    """Rows of 768 inputs (three steps of 256: an odd step count, whose last step starts two bytes into a dword in the
+    staged form) through switch_glu's tiles: gate/up 512 x 768, down 768 x 512, 16 experts, 256 tokens top-8,
+    float16, against the oracle's chain."""
+    experts, rows, cols, tokens, k = 16, 512, 768, 256, 8
+    layer = {n: Stack(kind, experts, r, c, 900 + i, gpu) for i, (n, (r, c)) in
+             enumerate((("gate", (rows, cols)), ("up", (rows, cols)), ("down", (cols, rows))))}
+    rng = np.random.default_rng(15)
+    idx = np.stack([rng.choice(experts, k, replace=False) for _ in range(tokens)])
+    x = (rng.standard_normal((tokens, cols)) / 16).astype(np.float16)
+    xs, ix = torch.from_numpy(x).to(gpu), torch.from_numpy(idx).to(gpu)
+    assert idx.size >= B.TILES_FROM
+    y = B.BlockSwitchGLU(layer["gate"].lin, layer["up"].lin, layer["down"].lin)(xs, ix)
+    y = y.float().cpu().numpy().reshape(-1, cols)
+    flat = idx.reshape(-1)
+    xr = x.astype(np.float64)
+    want = np.empty((len(flat), cols))
+    for e in np.unique(flat):
+        at = np.nonzero(flat == e)[0]
+        g = xr[at // k] @ layer["gate"].weights(e).astype(np.float64).T
+        u = xr[at // k] @ layer["up"].weights(e).astype(np.float64).T
+        h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32).astype(np.float16)  # float32 SwiGLU rounded once
+        want[at] = h.astype(np.float64) @ layer["down"].weights(e).astype(np.float64).T
+    assert rel_l2(y, as_dtype(want, torch.float16)) <= REL
 
 
 def test_prefill_routed_experts(gpu, iq3s_layer):

@@ -238,20 +238,27 @@ def test_gate_up_with_shared_expert(gpu, kind, pairs, rows, s_rows):
         idx[1] = experts + 2  # names no expert
     x = (rng.standard_normal((1, H)) / 64).astype(np.float16)
     xs, ix = torch.from_numpy(x).to(gpu), torch.from_numpy(idx).to(gpu)
-    got = B.gate_up_swiglu_shared(gate, up, xs, ix, sg, su)
+    got = B.gate_up_swiglu_shared(gate, up, xs, ix, sg, su, with_shared_gu=True)
     x2 = torch.from_numpy(np.repeat(x, 2, axis=0)).to(gpu)
     assert B.gate_up_swiglu_shared(gate, up, x2, torch.cat([ix, ix]), sg, su) is None  # two tokens
     if s_rows > pairs * rows:  # fewer waves than shared rows
         assert got is None
         return
-    gs, us, hs, sh = got
+    gs, us, hs, sh, sgk, suk = got
     torch.cuda.synchronize()
     for a, b in zip((gs, us, hs), B.gate_up_swiglu(gate, up, xs, ix, pairs)):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     xd = x.astype(np.float64)[0]
     gd, ud = (O.dequantize(lay.blocks.cpu().numpy(), "Q4_K", (s_rows, H)).astype(np.float64) @ xd for lay in (sg, su))
+    # the shared expert's own g and u from that launch at 1e-3 of the float64 products; h within two float16 steps
+    # of the SwiGLU of the launch's own g and u (strata_mlx/blocks.py:222-236), and at 2e-3 of the float64 chain
+    gk, uk = sgk.float().cpu().numpy()[0], suk.float().cpu().numpy()[0]
+    assert rel_l2(gk, gd) <= REL and rel_l2(uk, ud) <= REL
+    own = O.swiglu_rounded(sgk.cpu().numpy()[0], suk.cpu().numpy()[0], np.float16).astype(np.float64)
+    steps = np.abs(sh.cpu().numpy()[0].astype(np.float64) - own) / np.maximum(
+        np.spacing(np.abs(own.astype(np.float16))).astype(np.float64), 2.0 ** -24)
+    assert steps.max() <= 2.0
     want = O.swiglu_rounded(gd, ud, np.float16)
-    # g and u within 1e-3 of the float64 products, each rounded to float16, then the SwiGLU's three roundings
     assert rel_l2(sh.float().cpu().numpy()[0], want) <= 2e-3
     _, _, hd = D.gate_up_swiglu(sg, su, xs)
     assert rel_l2(sh.float().cpu().numpy()[0], hd.float().cpu().numpy()[0]) <= 2e-3

@@ -25,7 +25,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.strata_abi_version() == 2
+    assert lib.strata_abi_version() == 3
 
 
 @pytest.mark.parametrize("kind, per, size", [("Q2_0", 64, 18), ("IQ3_S", 256, 110), ("IQ3_XXS", 256, 98),
@@ -68,9 +68,12 @@ def test_arguments_are_checked_before_any_launch():
     assert gu(x3, 1, 1, 4, 64, 256, 1, None, 1, 1, 1, 16, 1, 0, None) == _lib.ERR_DTYPE  # float32 h
     assert gu(x3, 1, 1, 4, 64, 256, 1, None, 1, 1, 1, 8, 1, 1, None) == _lib.ERR_ARG  # tiles of 8
     assert gu(x3, 0, 1, 4, 64, 256, 1, None, 1, 1, 1, 16, 1, 1, None) == _lib.ERR_ARG  # null gate
+    # a matrix of 4 GiB or more (row offsets within a matrix are 32-bit in these kernels)
+    assert gu(x3, 1, 1, 4, 1 << 24, 4096, 1, None, 1, 1, 1, 16, 1, 1, None) == _lib.ERR_SHAPE
     dn = lib.strata_prompt_down
     assert dn(x3, 1, 4, 64, 256, 1, None, 1, 1, 16, 1, 1, -1, 1, 1, None) == _lib.ERR_ARG  # negative pairs
     assert dn(x3, 1, 4, 64, 256, 1, None, 1, 1, 16, 1, 0, 4, 1, 1, None) == _lib.ERR_ARG  # null idx
+    assert dn(x3, 1, 4, 1 << 24, 4096, 1, None, 1, 1, 16, 1, 1, 4, 1, 1, None) == _lib.ERR_SHAPE  # 4 GiB matrices
     na = lib.strata_route_tiles_noalloc
     assert na(1, 65537, 8, 256, 16, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # more pairs than its array takes
     assert na(1, 4096, 8, 1025, 16, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # more experts
