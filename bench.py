@@ -4,10 +4,10 @@
 Headline (value): routed-expert decode matvec, IQ3_S, 256 experts top-8 of Zipf(1.1) routing, gate/up 1536 x 4096
 and down 4096 x 1536 with the SwiGLU between them, float16 activations, batch 1. A step is one decode pass of the
 batch through 16 distinct routed-expert layers (about 1 GB of expert bytes, four times the 256 MB MALL), each a
-BlockSwitchGLU call as the engine makes it, captured once as a HIP graph and replayed; at one token a layer is one
-launch (gate, up, SwiGLU and down: strata_expert_layer). value = algorithmic bytes / time: the distinct experts'
-packed bytes plus activations in and out (x, h written and read, y). two_launches: the same layers as the
-gate+up+SwiGLU launch followed by the down launch.
+BlockSwitchGLU call as the engine makes it (the gate+up+SwiGLU launch, then the down launch), captured once as a HIP
+graph and replayed. value = algorithmic bytes / time: the distinct experts' packed bytes plus activations in and out
+(x, h written and read, y). one_launch: the same layers as one launch each (gate, up, SwiGLU and down:
+strata_expert_layer).
 
 Beside it, on the same line, the other workloads of the path:
   decode_t4      the same at 4 tokens (two launches a layer)
@@ -15,6 +15,7 @@ Beside it, on the same line, the other workloads of the path:
   q4k_matvec     one Q4_K 4096 x 4096 matrix, float32 x, batch 1 (graphs of 64 distinct copies), and its CPU path
   prompt         512-token prompt chunk, IQ3_XXS, 256 experts top-8, bfloat16: tiles on the GPU, the fused
                  gate/up/SwiGLU and scatter-down MFMA kernels; TFLOPS over the real pairs' 2 * pairs * 3 * H * F
+  prompt_q2_0    the same chunk in Q2_0 blocks
   dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K fused into one launch, o
                  Q8_0, the shared expert's Q4_K gate and up 1536 x 4096 with the SwiGLU in one launch and its
                  down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16 token each (graphs over copies, at least
@@ -22,12 +23,13 @@ Beside it, on the same line, the other workloads of the path:
                  routed gate+up launches instead (its marginal time over those launches alone)
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
                  the dense layers dequantized for the chunk and multiplied by the library product, TFLOPS
-  roofline       the dominant kernel (the one-launch layer): algorithmic bytes per launch / its mean duration
-                 (HIP events around the graph of those launches, on the stream they run on), against 8 TB/s
+  roofline       the dominant kernel (the gate+up+SwiGLU launch): algorithmic bytes per launch / its mean duration
+                 (HIP events around a graph of those launches only, on the stream they run on), against 8 TB/s
   cpu_baseline   the oracle's numpy decode of the touched experts (one thread) + float32 matvecs (BLAS on the
                  host's cores) on a few layers of the headline workload; q4k_matvec carries its own
 
---dense prints only dense_decode as its own line.
+--dense prints only dense_decode as its own line; --only NAME one other sub-workload (prompt, prompt_q2_0, prefill
+with two IQ3_S layers, q4k).
 """
 
 import argparse
@@ -59,6 +61,8 @@ def parse():
     ap.add_argument("--no-prompt", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline, decode_t4, roofline and prompt")
     ap.add_argument("--dense", action="store_true", help="only the dense half of a mixed-model decode token")
+    ap.add_argument("--only", choices=("prompt", "prompt_q2_0", "prefill", "q4k"),
+                    help="only this sub-workload, printed as its own line (for profiling one kernel family)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 512 MiB with torch's copy kernel three times: the known-size reference that "
                          "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -106,8 +110,9 @@ def decode_layers(B, synth, dev, layers, kind="IQ3_S", seed=0):
 
 def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
     """A step: every layer of `lins` called as the engine calls it (BlockSwitchGLU: the gate/up/SwiGLU launch, then
-    down). Returns (GB/s, ms per step, bytes per step, (mean bytes of a layer, mean seconds of a layer), routes, GB/s
-    of the same layers as one launch each (strata_expert_layer; None where it does not take the case))."""
+    down). Returns (GB/s, ms per step, bytes per step, (mean bytes of a gate/up launch, its mean seconds in a graph
+    of those launches alone), routes, GB/s of the same layers as one launch each (strata_expert_layer; None above
+    one token))."""
     routes = [synth.zipf_routing(tokens, E, K, rng)[0] for _ in lins]
     idx = [torch.from_numpy(r).to(torch.int32).to(dev) for r in routes]
     x = (torch.randn((tokens, H), device=dev)).half()
@@ -122,12 +127,16 @@ def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
         for (gate, up, down), ix in zip(lins, idx):
             B.expert_layer(gate, up, down, x, ix.reshape(-1))
 
+    def gate_up_only():
+        for (gate, up, down), ix in zip(lins, idx):
+            B.gate_up_swiglu(gate, up, x, ix.reshape(-1), K)
+
     one = tokens == 1
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     graphs = {}
     with torch.cuda.stream(stream):  # one eager pass first: the library's lazy state, torch's allocator
-        for name, run in (("layer", layered), ("one", one_launch))[:2 if one else 1]:
+        for name, run in (("layer", layered), ("gu", gate_up_only), ("one", one_launch))[:3 if one else 2]:
             run()
             torch.cuda.synchronize()
             graphs[name] = torch.cuda.CUDAGraph()
@@ -135,30 +144,34 @@ def decode_bench(B, synth, dev, lins, tokens, steps, warmup, rng):
                 run()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    step_bytes = 0
+    step_bytes, gu_bytes = 0, 0
     for r in routes:
         d = len(np.unique(r))
         # the distinct experts' gate, up and down; x in, h between the halves (written and read), y out
         step_bytes += d * 3 * mat_bytes + tokens * H * 2 + 2 * tokens * K * F * 2 + tokens * K * H * 2
+        gu_bytes += d * 2 * mat_bytes + tokens * H * 2 + tokens * K * F * 2  # gate/up launch: x in, h out
     t = time_graph(graphs["layer"], steps, warmup)
+    t_gu = time_graph(graphs["gu"], steps, warmup)
     gbs_one = None
     if one:
         gbs_one = step_bytes * steps / time_graph(graphs["one"], steps, warmup) / 1e9
         if B.layer_status(dev):
             raise RuntimeError("a wait of the one-launch layer gave up")
-    layer = (step_bytes / len(lins), t / steps / len(lins))
-    return step_bytes * steps / t / 1e9, t / steps * 1e3, step_bytes, layer, routes, gbs_one
+    gate_up = (gu_bytes / len(lins), t_gu / steps / len(lins))
+    return step_bytes * steps / t / 1e9, t / steps * 1e3, step_bytes, gate_up, routes, gbs_one
 
 
-def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512):
+def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512, kind="IQ3_XXS"):
+    """A 512-token prompt chunk of `layers` distinct expert layers in `kind` (256 experts top-8 of Zipf routing,
+    bfloat16 tokens) through switch_glu's tiles. TFLOPS over the real pairs' 2 * pairs * 3 * H * F, against the
+    dense MFMA peak and against the HBM ceiling of reading every expert's weights once."""
     g = torch.Generator(device=dev)
     g.manual_seed(1)
     lins = []
     for _ in range(layers):
-        mats = [synth.random_stack("IQ3_XXS", E * r * c, dev, g) for r, c in ((F, H), (F, H), (H, F))]
-        lins.append((B.BlockSwitchLinear(mats[0], "IQ3_XXS", (E, F, H)),
-                     B.BlockSwitchLinear(mats[1], "IQ3_XXS", (E, F, H)),
-                     B.BlockSwitchLinear(mats[2], "IQ3_XXS", (E, H, F))))
+        mats = [synth.random_stack(kind, E * r * c, dev, g) for r, c in ((F, H), (F, H), (H, F))]
+        lins.append((B.BlockSwitchLinear(mats[0], kind, (E, F, H)), B.BlockSwitchLinear(mats[1], kind, (E, F, H)),
+                     B.BlockSwitchLinear(mats[2], kind, (E, H, F))))
     idx = [torch.from_numpy(synth.zipf_routing(tokens, E, K, rng)[0]).to(torch.int32).to(dev) for _ in lins]
     x = torch.randn((tokens, H), device=dev).to(torch.bfloat16)
     for (gate, up, down), ix in zip(lins, idx):
@@ -171,9 +184,13 @@ def prompt_bench(B, synth, dev, steps, warmup, rng, layers=4, tokens=512):
     t = time_graph(graph, steps, warmup)
     flops = 2.0 * tokens * K * 3 * H * F * layers
     tflops = flops * steps / t / 1e12
-    return {"workload": "prompt chunk 512 tokens, IQ3_XXS, 256 experts top-8, bf16", "tflops": round(tflops, 2),
+    per, bb = synth.BLOCK[kind]
+    ceiling = 2.0 * tokens * K * 3 * H * F / (3 * E * F * H / per * bb) * HBM_PEAK_GBS / 1e3
+    del lins
+    torch.cuda.empty_cache()
+    return {"workload": f"prompt chunk {tokens} tokens, {kind}, 256 experts top-8, bf16", "tflops": round(tflops, 2),
             "ms_per_layer": round(t / steps / layers * 1e3, 4), "mfma_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "hbm_bound_tflops": round(2.0 * tokens * K * 3 * H * F / (3 * E * F * H / 256 * 98) * HBM_PEAK_GBS / 1e3, 1)}
+            "hbm_bound_tflops": round(ceiling, 1), "hbm_bound_frac": round(tflops / ceiling, 4)}
 
 
 # The dense layers of a mixed-model decode token, as an engine runs them: q, k and v fused into one 12288-row
@@ -441,15 +458,26 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only:
+        note(f"only {args.only}")
+        steps = max(2, args.steps // 10)
+        if args.only in ("prompt", "prompt_q2_0"):
+            out = prompt_bench(B, synth, dev, steps, 2, rng, kind="Q2_0" if args.only == "prompt_q2_0" else "IQ3_XXS")
+        elif args.only == "q4k":
+            out = q4k_bench(B, synth, dev, max(2, args.steps // 5), 2)
+        else:
+            from strata_mlx_amd import dense as D
+            out = prefill_bench(B, D, synth, dev, decode_layers(B, synth, dev, 2), steps, 2, rng)
+        print(json.dumps({args.only: out}))
+        return
     note(f"making {args.layers} IQ3_S layers of 256 experts")
     lins = decode_layers(B, synth, dev, args.layers)
     note("decode, batch {}".format(args.tokens))
-    gbs, ms, step_bytes, (lay_bytes, lay_s), routes, gbs_one = decode_bench(B, synth, dev, lins, args.tokens,
-                                                                             args.steps, args.warmup, rng)
+    gbs, ms, step_bytes, (gu_bytes, gu_s), routes, gbs_one = decode_bench(B, synth, dev, lins, args.tokens,
+                                                                           args.steps, args.warmup, rng)
     note(f"decode: {gbs:.1f} GB/s (one launch a layer: {gbs_one}); batch 4")
     gbs4, ms4, _, _, _, _ = decode_bench(B, synth, dev, lins, 4, args.steps, args.warmup, rng)
-    achieved = lay_bytes / lay_s / 1e9
-    one = args.tokens == 1
+    achieved = gu_bytes / gu_s / 1e9
     result = {
         "metric": "expert decode matvec GB/s (% HBM peak) + prompt dequant-GEMM TFLOPS",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -460,7 +488,7 @@ def main():
                 "no launch's timing depends on (the parity tests run the same launches at x ~ N(0,1)/64)",
         "config": {"workload": f"routed-expert decode, IQ3_S, 256 experts top-8, gate/up 1536x4096, down 4096x1536, "
                                f"SwiGLU, batch {args.tokens}; a step = {args.layers} distinct layers, each one "
-                               f"BlockSwitchGLU call" + (" (one launch)" if one else ""),
+                               f"BlockSwitchGLU call (gate/up/SwiGLU, then down)",
                    "tokens": args.tokens, "experts": E, "top_k": K, "hidden": H, "ffn": F, "layers": args.layers,
                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
         "one_launch": None if gbs_one is None else {
@@ -471,9 +499,8 @@ def main():
                       "note": "gate/up/SwiGLU then down, two launches a layer"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": ("routed_layer_kernel IQ3_S: gate, up, SwiGLU and down of one token, one launch a "
-                                "layer (strata_expert_layer)") if one else "the layer's two launches",
-                     "bytes_per_launch": int(lay_bytes), "mean_launch_us": round(lay_s * 1e6, 3)},
+                     "kernel": "routed_glu_kernel IQ3_S gate+up+SwiGLU (strata_expert_gate_up_swiglu)",
+                     "bytes_per_launch": int(gu_bytes), "mean_launch_us": round(gu_s * 1e6, 3)},
     }
     if not args.no_extra:
         note("speculative verify, Q2_0, 5 rows")
@@ -488,6 +515,8 @@ def main():
     if not args.no_prompt:
         note("prompt chunk")
         result["prompt"] = prompt_bench(B, synth, dev, max(2, args.steps // 10), 2, rng)
+        note("prompt chunk, Q2_0")
+        result["prompt_q2_0"] = prompt_bench(B, synth, dev, max(2, args.steps // 10), 2, rng, kind="Q2_0")
     if not args.no_extra:
         note("dense half of a decode token")
         dd = dense_bench(B, synth, dev, max(2, args.steps // 5), 2)

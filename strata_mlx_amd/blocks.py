@@ -71,8 +71,9 @@ def _idx32(indices: torch.Tensor) -> torch.Tensor:
 
 
 class BlockSwitchLinear:
-    """A stack of linear layers kept as the file's blocks; called like mlx-lm's `QuantizedSwitchLinear`.
-    strata_mlx/blocks.py:525-558."""
+    """The experts' matrices of one projection (gate, up or down) as the GGUF bytes of an (experts, out, in) stack
+    on the GPU, with the call signature of mlx-lm's routed linear: each (token, expert) pair multiplies its token's
+    row by its expert's matrix. strata_mlx/blocks.py:525-558."""
 
     unpack_from = 5000  # pairs from which the reference multiplies unpacked floats; here a kernel either way
 
@@ -569,10 +570,10 @@ def _route(indices: torch.Tensor, experts: int) -> tuple:
 
 
 def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
-    """The pairs of `indices` (..., k) laid out in tiles of TOKENS_TILE, each tile one expert's, worked out on the
-    GPU with no host wait: (the expert of each tile, or `experts` for a tile nothing fills; the token of each slot;
-    the slot of each pair), int32, in P // 16 + min(E, P) tiles whatever the routing. An expert's slots go in
-    pair order. strata_mlx/blocks.py:657-681."""
+    """Groups a prompt's (token, expert) pairs by expert into tiles of TOKENS_TILE slots, on the GPU and without
+    waiting for it. Returns three int32 arrays: tile -> expert (`experts` marks an unused tile), slot -> token, and
+    pair -> slot. The tile count, P // 16 + min(E, P), is fixed by the pair count alone, so no routing can overflow
+    it. Within an expert, slots follow the pairs' order. strata_mlx/blocks.py:657-681."""
     return _route(indices, experts)[:3]
 
 
@@ -607,11 +608,11 @@ def rows_from_f32(c: torch.Tensor, row_max: torch.Tensor, dtype: torch.dtype) ->
 
 def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, tile_expert: torch.Tensor,
                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """out[p] = W[expert of p's tile] . a[p] for a stack `blocks` of `shape` (experts, rows, cols), on MFMA.
+    """The grouped product of a prompt's tiles on MFMA: row p of the result is W[e] . a[p], e the expert that p's
+    tile belongs to, W the (experts, rows, cols) stack in `blocks`.
 
-    a (P, cols), P a multiple of TOKENS_TILE, every TOKENS_TILE rows for one expert; tile_expert (P / 16,) says
-    which, or names no expert (>= experts) for a tile to leave out: its rows of the result are then whatever was
-    in memory (in `out` if given). float16 activations multiply weights as float16 (exact for IQ3_S / IQ3_XXS /
+    a has P rows of cols activations, P a whole number of tiles; tile_expert holds one expert per tile. A tile whose
+    entry is experts or more is skipped, and its rows of the result keep what the buffer held (`out`, when given). float16 activations multiply weights as float16 (exact for IQ3_S / IQ3_XXS /
     Q2_0 rows of whole 256-weight steps: integer codes times the run's own scale, with d on the float32 sums;
     rounded to float16 for the other types); bfloat16 rows are first scaled into float16 by a power of two each
     (rows_to_f16) and the sums scaled back, so they multiply exactly too; float32 activations multiply exact

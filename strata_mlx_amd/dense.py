@@ -46,10 +46,10 @@ def q6k_blocks(codes: torch.Tensor, scales: torch.Tensor, d: torch.Tensor) -> to
 
 
 class BlockLinear:
-    """A linear layer held as the file's blocks; called like `nn.Linear`. strata_mlx/dense.py:205-242.
-
-    `blocks` are the rows in the order of the layer's outputs. `inputs`, if given, is where in the file's row
-    each input is: the activations are reordered to the file's order before they multiply."""
+    """A dense projection (attention, a shared expert, lm_head) whose weight rows stay GGUF blocks on the GPU, one
+    row per output, with nn.Linear's call (x (..., in) -> (..., out)). When the file stores the inputs in another
+    order, `inputs` gives each input's column in the file's row, and x is permuted to match before the product.
+    strata_mlx/dense.py:205-242."""
 
     def __init__(self, blocks: torch.Tensor, kind: str, shape: tuple, inputs=None):
         self.blocks, self.kind = B._flat_u8(blocks), kind
@@ -186,8 +186,8 @@ class ScaledLinear(BlockLinear):
 
 
 class BlockEmbedding:
-    """An embedding held as the file's blocks; a token's row is decoded when the token comes.
-    strata_mlx/dense.py:245-258."""
+    """Token embeddings left as GGUF blocks on the GPU: looking tokens up decodes just their rows, so the table is
+    never expanded to floats. strata_mlx/dense.py:245-258."""
 
     def __init__(self, blocks: torch.Tensor, kind: str, shape: tuple, dtype: torch.dtype):
         self.num_embeddings, self.dims = shape
