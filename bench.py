@@ -446,11 +446,6 @@ def main():
     def note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
-    if args.dense:
-        note("dense half of a mixed-model decode token")
-        print(json.dumps(dense_bench(B, synth, dev, max(2, args.steps // 5), 2)))
-        return
-
     if args.copy_probe:
         src = torch.ones(512 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -458,6 +453,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.dense:
+        note("dense half of a mixed-model decode token")
+        print(json.dumps(dense_bench(B, synth, dev, max(2, args.steps // 5), 2)))
+        return
+
     if args.only:
         note(f"only {args.only}")
         steps = max(2, args.steps // 10)

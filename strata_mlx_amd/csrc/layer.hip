@@ -70,10 +70,18 @@ __global__ __launch_bounds__(kGluThreads, 1) void routed_layer_kernel(LayerParam
   constexpr int kTabBytes = (8 * R::kEntries + 15) / 16 * 16;
   constexpr int kHPieces = 8 * 8 * S;  // h as down's token: 16-byte pieces
   __shared__ __attribute__((aligned(16))) uint8_t lds[kTabBytes + 16 * 512 + 16 * kHPieces + 16];
+  // down units a wave may claim (twice its share where the registers hold them: rows of 1536 inputs, one unit a
+  // wave), and a workgroup's
+  constexpr int kClaim = S == 3 && DUPW == 1 ? 2 : DUPW, kUnits = kGluWaves * DUPW;
   u32x2* const tab = reinterpret_cast<u32x2*>(lds);
   u32x4* const xs = reinterpret_cast<u32x4*>(lds + kTabBytes);
   u32x4* const hs = reinterpret_cast<u32x4*>(lds + kTabBytes + 16 * 512);
+  // the workgroup's words: whether a wait gave up, waves whose gate/up loads are all out, down units claimed, and the
+  // first wave that claimed none
   uint32_t* const gave_up = reinterpret_cast<uint32_t*>(lds + kTabBytes + 16 * 512 + 16 * kHPieces);
+  uint32_t* const issued = gave_up + 1;
+  uint32_t* const claimed = gave_up + 2;
+  uint32_t* const poller = gave_up + 3;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int group = blockIdx.x;
   uint32_t* const count = p.ws + kLayerCountAt + group;
@@ -94,7 +102,12 @@ __global__ __launch_bounds__(kGluThreads, 1) void routed_layer_kernel(LayerParam
   const int64_t expert = bad ? 0 : (int64_t)e;
   R::fill(tab, tid, entry);
   xs[x_piece_slot(c)] = xpiece;
-  if (tid == 0) *gave_up = 0;
+  if (tid == 0) {
+    *gave_up = 0;
+    *issued = 0;
+    *claimed = 0;
+    *poller = kGluWaves;
+  }
   __syncthreads();
   uint32_t x[32];
 #pragma unroll
@@ -128,6 +141,7 @@ __global__ __launch_bounds__(kGluThreads, 1) void routed_layer_kernel(LayerParam
   Fields f[kBuffers][2];
 #pragma unroll
   for (int k = 0; k < kBuffers; ++k) issue(k, f[k]);
+  if (UPW <= kBuffers && lane == 0) atomicAdd(issued, 1u);  // this wave's gate/up loads are all out
   float xsum[R::kPrepSums + 1];
   R::prep_x(x, xsum);
   float gv = 0.0f, uv = 0.0f;  // lane k: unit k's two totals
@@ -135,7 +149,10 @@ __global__ __launch_bounds__(kGluThreads, 1) void routed_layer_kernel(LayerParam
   for (int k = 0; k < UPW; ++k) {
     float g, u;
     glu_unit<KIND>(f[k % kBuffers], lane, x, x, xsum, xsum, tab, g, u);
-    if (k + kBuffers < UPW) issue(k + kBuffers, f[k % kBuffers]);
+    if (k + kBuffers < UPW) {
+      issue(k + kBuffers, f[k % kBuffers]);
+      if (k + kBuffers == UPW - 1 && lane == 0) atomicAdd(issued, 1u);
+    }
     gv = lane == k ? g : gv;
     uv = lane == k ? u : uv;
   }
@@ -165,27 +182,45 @@ __global__ __launch_bounds__(kGluThreads, 1) void routed_layer_kernel(LayerParam
     }
   }
 
-  // down's rows for this wave, asked for now: 8 lanes a row, lane m its run pairs m, m + 8, ...
+  // Down's rows. The workgroup's units (8 rows each) go to the waves that finish gate/up first, up to kClaim a wave,
+  // so that the rows of the last waves' units are not asked for last; and none before every wave's gate/up rows
+  // are asked for (down's rows would otherwise go out ahead of them). 8 lanes a row, lane m its run pairs m,
+  // m + 8, ... A wave that claims nothing has no loads in flight at the handover: the first such wave polls.
+  {
+    int n = 0;
+    while (__hip_atomic_load(issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)kGluWaves &&
+           ++n < (1 << 22))
+      __builtin_amdgcn_s_sleep(1);
+  }
   const int m = lane & 7, sub = lane >> 3;
   const uint8_t* const dmat = p.down + expert * p.dn_mat_bytes;
-  int r0[DUPW];
-  Fields fd[DUPW][S];
+  uint32_t base = 0;
+  if (lane == 0) base = atomicAdd(claimed, (uint32_t)kClaim);
+  base = __builtin_amdgcn_readfirstlane(base);
+  if (base >= (uint32_t)kUnits && lane == 0) atomicMin(poller, (uint32_t)wave);
+  int r0[kClaim];
+  bool dl[kClaim];
+  Fields fd[kClaim][S];
 #pragma unroll
-  for (int k = 0; k < DUPW; ++k) {
-    r0[k] = (q * DUPW + k) * 8;
-    const int rl = min(r0[k] + sub, p.dn_rows - 1);  // rows past the matrix read its last row, and write nothing
-    const uint8_t* rowp = dmat + (int64_t)rl * p.dn_row_bytes;
+  for (int k = 0; k < kClaim; ++k) {
+    dl[k] = base + k < (uint32_t)kUnits;
+    r0[k] = (slot * kUnits + (int)base + k) * 8;
+    if (dl[k]) {
+      const int rl = min(r0[k] + sub, p.dn_rows - 1);  // rows past the matrix read its last row, and write nothing
+      const uint8_t* rowp = dmat + (int64_t)rl * p.dn_row_bytes;
 #pragma unroll
-    for (int st = 0; st < S; ++st) R::load(rowp, 8 * st + m, fd[k][st]);
+      for (int st = 0; st < S; ++st) R::load(rowp, 8 * st + m, fd[k][st]);
+    }
     asm volatile("" ::: "memory");
   }
 
-  // every wave's h is out: the workgroup's flag says so (a hint: the tags decide). Wave 0 then waits for the flags
+  // every wave's h is out: the workgroup's flag says so (a hint: the tags decide). One wave then waits for the flags
   // of the pair's other workgroups, a few cache lines a poll, before the words themselves are read.
   __syncthreads();
   uint32_t* const flags = p.ws + kLayerFlagsAt + pair * p.slots;
   if (tid == 0) __hip_atomic_store(flags + slot, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (wave == 0) {
+  const uint32_t pw = *poller;
+  if ((uint32_t)wave == (pw < (uint32_t)kGluWaves ? pw : 0u)) {
     bool failed = false;
     for (int s0 = 0; s0 < p.slots; s0 += 64) {
       if (s0 + lane < p.slots) {
@@ -228,9 +263,10 @@ __global__ __launch_bounds__(kGluThreads, 1) void routed_layer_kernel(LayerParam
   const bool lost = *gave_up != 0;
   if (lost && tid == 0) __hip_atomic_fetch_or(p.ws, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // down: each unit's 8 rows against the pair's h
+  // down: each claimed unit's 8 rows against the pair's h
 #pragma unroll
-  for (int k = 0; k < DUPW; ++k) {
+  for (int k = 0; k < kClaim; ++k) {
+    if (!dl[k]) continue;
     float acc = 0.0f;
 #pragma unroll
     for (int st = 0; st < S; ++st) {
@@ -283,7 +319,8 @@ int launch_layer(LayerParams& p, hipStream_t s) {
   if (!upw || dneed > 2) return STRATA_ERR_SHAPE;
   if (p.ffn == 1536)
     return dneed == 1 ? launch_layer_u<KIND, 3, 1>(p, upw, groups, s) : launch_layer_u<KIND, 3, 2>(p, upw, groups, s);
-  return dneed == 1 ? launch_layer_u<KIND, 5, 1>(p, upw, groups, s) : launch_layer_u<KIND, 5, 2>(p, upw, groups, s);
+  // rows of 2560 inputs at two down units a wave spill registers: those go to the two launches
+  return dneed == 1 ? launch_layer_u<KIND, 5, 1>(p, upw, groups, s) : STRATA_ERR_SHAPE;
 }
 
 }  // namespace strata_mv

@@ -56,7 +56,7 @@ def test_layer_is_the_two_launches(gpu, layers, kind, ffn, pairs):
     ix = torch.from_numpy(idx).to(gpu)
     x = token(pairs, 1 / 64, gpu)
     got = B.expert_layer(gate, up, down, x, ix, with_h=True)
-    if ffn == 2560 and pairs >= 12:  # more than six gate/up rows a wave: not taken
+    if ffn == 2560 and pairs > 8:  # more than one down unit a wave on rows of 2560 inputs: not taken
         assert got is None
         return
     y, h = got
