@@ -91,10 +91,12 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
  * as strata_expert_gate_up_swiglu rounds it, then out[p, :] = down[idx[p]] . h[p, :]; the same bits as those two
  * calls (strata_expert_gate_up_swiglu, then strata_expert_matvec on down). gate, up (experts, ffn, hidden) and down
  * (experts, hidden, ffn) stacks of `kind` IQ3_S or Q2_0, hidden 4096, ffn 1536 or 2560; x one float16 token;
- * pairs 1 to 16; out (pairs, hidden) float16; out_h (pairs, ffn) float16 or NULL. A pair naming no expert gets
- * NaN rows. `workspace`: device memory of strata_expert_layer_workspace(pairs, ffn) bytes, zeroed before its first
- * call and then given to every call of that shape on one device and one stream (calls that share a workspace
- * must not overlap). One workgroup a CU runs for the launch and the workgroups of a pair wait for each other's h:
+ * pairs 1 to 16 (ffn 2560: 1 to 8 on a 256-CU part; more return STRATA_ERR_SHAPE and the caller makes the two
+ * calls); out (pairs, hidden) float16; out_h (pairs, ffn) float16 or NULL. A pair naming no expert gets NaN rows.
+ * `workspace`: device memory of strata_expert_layer_workspace(pairs, ffn) bytes for the largest (pairs, ffn) it
+ * serves, zeroed before its first call; calls of any shape on one device may then share it one after another
+ * (every call advances every workgroup's launch count; calls that share a workspace must not overlap). One
+ * workgroup a CU runs for the launch and the workgroups of a pair wait for each other's h:
  * each wait gives up after `spin` polls of memory (about a microsecond each; 100000 is ample), writes NaN to its
  * rows of out and sets bit 0 of the workspace's first uint32, which the caller reads and clears. Replaces the
  * per-pair path of switch_glu at one token, strata_mlx/blocks.py:958-986 (the gate and up calls, then matvec_glu's
