@@ -1345,6 +1345,7 @@ int launch_direct(MatvecParams& p, bool one_token, int grid_y, int grid_z, hipSt
 }  // namespace strata_mv
 
 #include "routed_impl.h"
+#include "stream_impl.h"
 
 namespace strata_mv {
 
@@ -1370,6 +1371,7 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
       const bool one = p.mode == MODE_PTRS || (p.mode == MODE_DENSE ? p.tokens == 1
                                                                      : (glu ? p.pairs <= 16
                                                                             : p.pairs <= p.share || p.pairs <= 8));
+      if (!glu && stream_takes<KIND>(p, grid_y)) return launch_stream<KIND>(p, s);
       if (!glu && routed_one_takes<KIND>(p)) return launch_routed_one<KIND>(p, s);
       if (p.glu_out != nullptr) {
         if (!glu && grid_z == 2 && routed_glu_takes<KIND>(p)) return launch_routed_glu<KIND>(p, s);
