@@ -108,14 +108,22 @@ __device__ __forceinline__ void put_signs(uint32_t s8, const u32x2& g0, const u3
   w[3] = (m3 & 0x80008000u) | g1[1];
 }
 
-// Group pair l (weights 8 l .. 8 l + 7) of run h of the lane's run pair g, IQ3_XXS or IQ3_S: 4 packed float16
-// pairs, the run's scale and signs folded in (exact). What the four group pairs of a run share is the same
+// Group pair l (weights 8 l .. 8 l + 7) of run h of the lane's run pair g, IQ3_XXS, IQ3_S or Q2_0: 4 packed
+// float16 pairs, the run's scale and signs folded in (exact). What the four group pairs of a run share is the same
 // expression for each, computed once where they are unrolled together.
 template <int KIND>
 __device__ __forceinline__ void decode_folded4(const RunPair<KIND>& f, int h, int g, int l, uint32_t (&w)[4],
                                                const DirectTables<KIND>& t) {
-  static_assert(KIND == K_IQ3_XXS || KIND == K_IQ3_S, "the codebook types");
-  if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116: groups 2l, 2l + 1, signs ksigns[7 bits of aux]
+  static_assert(KIND == K_IQ3_XXS || KIND == K_IQ3_S || KIND == K_Q2_0, "the staged types");
+  if constexpr (KIND == K_Q2_0) {  // strata_mlx/blocks.py:58-68: code bytes 2 l, 2 l + 1 of the run, four (c - 1) each
+    const uint32_t q = f.qs[2 * h + (l >> 1)];
+    const u32x2 c0 = t.q2[(q >> (16 * (l & 1))) & 255];
+    const u32x2 c1 = t.q2[(q >> (16 * (l & 1) + 8)) & 255];
+    w[0] = c0[0];
+    w[1] = c0[1];
+    w[2] = c1[0];
+    w[3] = c1[1];
+  } else if constexpr (KIND == K_IQ3_XXS) {  // strata_mlx/blocks.py:103-116: groups 2l, 2l + 1, signs ksigns[7 bits of aux]
     const uint32_t q = f.qs[2 * h + (l >> 1)];
     const u32x2 g0 = t.grid[(q >> (16 * (l & 1))) & 255];
     const u32x2 g1 = t.grid[(q >> (16 * (l & 1) + 8)) & 255];
@@ -360,14 +368,17 @@ __device__ __forceinline__ void run_chunk(const PromptParams& p, const DirectTab
 // on a CU; at two (a third row buffer, or the IQ3_XXS codebook with its signs folded in, 32 KB) or at four (128
 // registers, spilled) the kernel ran slower.
 template <int KIND>
-constexpr bool kStagedKind = KIND == K_IQ3_S || KIND == K_IQ3_XXS;
+constexpr bool kStagedKind = KIND == K_IQ3_S || KIND == K_IQ3_XXS || KIND == K_Q2_0;
 template <int KIND>
-constexpr int kStepBytes = KIND == K_IQ3_S ? 110 : 98;
+constexpr int kStepBytes = KIND == K_IQ3_S ? 110 : KIND == K_IQ3_XXS ? 98 : 72;  // Q2_0: four 18-byte blocks
 template <int KIND>
-constexpr int kSlotDwords = (kStepBytes<KIND> + 2) / 4;  // dwords a row's step spans: 28, 25
-constexpr int kSlotPitch = 28;                            // dwords a row's slot (112 bytes)
-constexpr int kGroupLoads = 16 * kSlotPitch / 64;         // wave instructions a group of 16 rows: 7
-constexpr int kGroupBytes = 256 * kGroupLoads;            // a group's buffer
+constexpr int kSlotDwords = (kStepBytes<KIND> + 2) / 4;  // dwords a row's step spans: 28, 25, 18
+template <int KIND>
+constexpr int kSlotPitch = KIND == K_Q2_0 ? 20 : 28;     // dwords a row's slot (112 bytes; Q2_0 80)
+template <int KIND>
+constexpr int kGroupLoads = 16 * kSlotPitch<KIND> / 64;  // wave instructions a group of 16 rows: 7 (Q2_0 5)
+template <int KIND>
+constexpr int kGroupBytes = 256 * kGroupLoads<KIND>;     // a group's buffer
 
 // lane l's dword at base + voff into LDS at lds + 4 l (the wave's LDS address in M0, which the load reads when
 // it issues). M0 is the compiler's register: its value is kept in an SGPR and put back after the load, so the
@@ -413,14 +424,24 @@ __device__ __forceinline__ u32x2 lds_8(const uint8_t* base, uint32_t a0) {
 template <int KIND, int S>
 __device__ __forceinline__ void lds_fields(const uint8_t* slot, int g, RunPair<KIND>& f) {
   const uint32_t gg = (uint32_t)g;
-  f.d = lds_at<uint16_t>(slot, S);
-  f.qs = lds_16<S + 2>(slot, 16 * gg);
-  if constexpr (KIND == K_IQ3_S) {
-    f.qh = lds_at<uint16_t>(slot, S + 66 + 2 * gg);
-    f.sg = lds_8<S + 2>(slot, 72 + 8 * gg);
-    f.sc = lds_at<uint16_t>(slot, S + 106 + 2 * (gg >> 1));
+  if constexpr (KIND == K_Q2_0) {  // a step is 72 bytes from a dword (S unused): block g's d @18 g, qs @18 g + 2
+    const uint32_t o = 18u * gg, q = o + 2u, a = q & ~3u, sh = q & 3u;
+    f.d = lds_at<uint16_t>(slot, o);
+    uint32_t dw[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) dw[k] = lds_at<uint32_t>(slot, a + 4u * k);
+    f.qs = u32x4{__builtin_amdgcn_alignbyte(dw[1], dw[0], sh), __builtin_amdgcn_alignbyte(dw[2], dw[1], sh),
+                 __builtin_amdgcn_alignbyte(dw[3], dw[2], sh), __builtin_amdgcn_alignbyte(dw[4], dw[3], sh)};
   } else {
-    f.aux = lds_8<S + 2>(slot, 64 + 8 * gg);
+    f.d = lds_at<uint16_t>(slot, S);
+    f.qs = lds_16<S + 2>(slot, 16 * gg);
+    if constexpr (KIND == K_IQ3_S) {
+      f.qh = lds_at<uint16_t>(slot, S + 66 + 2 * gg);
+      f.sg = lds_8<S + 2>(slot, 72 + 8 * gg);
+      f.sc = lds_at<uint16_t>(slot, S + 106 + 2 * (gg >> 1));
+    } else {
+      f.aux = lds_8<S + 2>(slot, 64 + 8 * gg);
+    }
   }
 }
 
@@ -441,8 +462,9 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
   constexpr int kChunks = NTC * 16 * (kStep / 8);
   constexpr int kLoads = kChunks / kThreadsWg;
   static_assert(kChunks % kThreadsWg == 0, "whole pieces a thread");
-  static_assert(kStagedKind<KIND>, "staged rows: IQ3_S, IQ3_XXS");
-  constexpr int kSB = kStepBytes<KIND>, kDW = kSlotDwords<KIND>, kGL = kGroupLoads;
+  static_assert(kStagedKind<KIND>, "staged rows: IQ3_S, IQ3_XXS, Q2_0");
+  constexpr int kSB = kStepBytes<KIND>, kDW = kSlotDwords<KIND>, kGL = kGroupLoads<KIND>, kPitchDw = kSlotPitch<KIND>;
+  constexpr int kGB = kGroupBytes<KIND>;
   constexpr int kABuf = NT * 16 * kPitch;  // float16: an activation buffer
   constexpr int kABufs = activation_buffers<NT>();
   const int lane = tid & 63;
@@ -463,7 +485,7 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
 #pragma unroll
     for (int i = 0; i < kGL; ++i) {
       const int f = 64 * i + lane;
-      const int q = f / kSlotPitch, d = min(f % kSlotPitch, kDW - 1);
+      const int q = f / kPitchDw, d = min(f % kPitchDw, kDW - 1);
       voff[grp][i] = (uint32_t)min(grow[grp] + q, p.rows - 1) * (uint32_t)p.row_bytes + 4u * (uint32_t)d;
     }
   const uint32_t w_base = (uint32_t)(uintptr_t)w_lds;
@@ -472,7 +494,7 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
 #pragma unroll
     for (int grp = 0; grp < 2; ++grp) {
       const uint8_t* base = mat[grp] + first;
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(w_base + (uint32_t)((wave * 2 + grp) * kGroupBytes));
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(w_base + (uint32_t)((wave * 2 + grp) * kGB));
 #pragma unroll
       for (int i = 0; i < kGL; ++i) dma_dword(base, voff[grp][i], dst + 256u * i);
     }
@@ -528,8 +550,8 @@ __device__ __forceinline__ void run_chunk_staged(const PromptParams& p, const Di
         RunPair<KIND> f[2];
 #pragma unroll
         for (int grp = 0; grp < 2; ++grp) {
-          const uint8_t* slot = reinterpret_cast<const uint8_t*>(w_lds) + (wave * 2 + grp) * kGroupBytes +
-                                4 * kSlotPitch * n;
+          const uint8_t* slot = reinterpret_cast<const uint8_t*>(w_lds) + (wave * 2 + grp) * kGB +
+                                4 * kPitchDw * n;
           if (sp == 0)  // k even: the step starts at a dword; odd: 2 bytes in (kSB is 2 mod 4)
             lds_fields<KIND, 0>(slot, g, f[grp]);
           else
@@ -612,7 +634,7 @@ template <int KIND, int MODE, typename OT, int WAVES, int NT, bool STAGED>
 __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptParams p) {
   constexpr int kThreadsWg = 64 * WAVES;
   constexpr bool kStagedHere = STAGED && kStagedKind<KIND>;
-  __shared__ __attribute__((aligned(16))) uint8_t w_lds[kStagedHere ? WAVES * 2 * kGroupBytes : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t w_lds[kStagedHere ? WAVES * 2 * kGroupBytes<KIND> : 16];
   __shared__ DirectTables<KIND> tab;
   __shared__ __attribute__((aligned(16))) f16 a_lds[(kStagedHere ? activation_buffers<NT>() : 1) * NT * 16 * kPitch];
 
