@@ -20,7 +20,8 @@ Beside it, on the same line, the other workloads of the path:
                  Q8_0, the shared expert's Q4_K gate and up 1536 x 4096 with the SwiGLU in one launch and its
                  down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16 token each (graphs over copies, at least
                  1 GB a graph); shared_in_routed: the shared expert's gate and up taken by the headline layers'
-                 routed gate+up launches instead (its marginal time over those launches alone)
+                 routed gate+up launches instead (its marginal time over those launches alone);
+                 shared_down_in_routed: its down taken by the layers' routed down launches the same way
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
                  the dense layers dequantized for the chunk and multiplied by the library product, TFLOPS
   roofline       the dominant kernel (the gate+up+SwiGLU launch): algorithmic bytes per launch / its mean duration
@@ -292,6 +293,58 @@ def shared_fused_bench(B, D, synth, dev, lins, steps, warmup, rng):
             "fused_hbm_frac": round((routed_bytes + shared_bytes) / (us["fused"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def shared_down_bench(B, D, synth, dev, lins, steps, warmup, rng):
+    """One decode token's routed down (the layers' IQ3_S stacks, 4096 x 1536, 256 experts top-8) with a shared
+    expert's Q4_K down (4096 x 1536) in the same launch (blocks.expert_matvec_shared), against the routed launch
+    alone and the two launches apart: the shared down's marginal time a layer and its bytes' rate over it."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    routes = [synth.zipf_routing(1, E, K, rng)[0] for _ in lins]
+    idx = [torch.from_numpy(r).to(torch.int32).to(dev).reshape(-1) for r in routes]
+    h = (torch.randn((K, F), device=dev) / 8).half()
+    sx = (torch.randn((1, F), device=dev) / 8).half()
+    shared = [D.BlockLinear(synth.random_stack("Q4_K", H * F, dev, g), "Q4_K", (H, F)) for _ in lins]
+    calls = [B.expert_matvec_shared(down, ix, sd) for (_, _, down), ix, sd in zip(lins, idx, shared)]
+
+    def alone():
+        for (_, _, down), ix in zip(lins, idx):
+            B.expert_matvec(down, ix, h)
+
+    def apart():
+        for (_, _, down), ix, sd in zip(lins, idx, shared):
+            B.expert_matvec(down, ix, h)
+            B.window_matvec(sd.blocks, "Q4_K", H, F, sx)
+
+    def fused():
+        for call in calls:
+            if call(h, sx) is None:
+                raise RuntimeError("the routed down launch did not take the shared expert")
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):  # one eager pass of each first: the library's lazy state, torch's allocator
+        for run in (alone, apart, fused):
+            run()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graphs = {}
+    for name, run in (("alone", alone), ("apart", apart), ("fused", fused)):
+        graphs[name] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[name]):
+            run()
+    us = {name: time_graph(gr, steps, warmup) / steps / len(lins) * 1e6 for name, gr in graphs.items()}
+    mat_bytes = lins[0][2].blocks.numel() // E
+    routed_bytes = sum(len(np.unique(r)) * mat_bytes for r in routes) / len(lins) + K * F * 2 + K * H * 2
+    shared_bytes = shared[0].blocks.numel() + F * 2 + H * 2  # its rows and token in, its rows' sums out
+    marginal = us["fused"] - us["alone"]
+    return {"workload": f"one decode token's down, {len(lins)} layers: routed IQ3_S 256 experts top-8 {H} x {F} + "
+                        f"shared expert Q4_K {H} x {F}",
+            "routed_us": round(us["alone"], 3), "apart_us": round(us["apart"], 3), "fused_us": round(us["fused"], 3),
+            "shared_bytes": int(shared_bytes), "shared_marginal_us": round(marginal, 3),
+            "shared_hbm_frac": round(shared_bytes / (marginal * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if marginal > 0 else None,
+            "fused_hbm_frac": round((routed_bytes + shared_bytes) / (us["fused"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def host_cpu():
     """(the host's cores as this process sees them, the threads BLAS is given, the CPU model)."""
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -526,6 +579,9 @@ def main():
         note("shared expert's gate and up in the routed launch")
         result["dense_decode"]["shared_in_routed"] = shared_fused_bench(B, D, synth, dev, lins, args.steps, args.warmup,
                                                                         rng)
+        note("shared expert's down in the routed down launch")
+        result["dense_decode"]["shared_down_in_routed"] = shared_down_bench(B, D, synth, dev, lins, args.steps,
+                                                                            args.warmup, rng)
         note("2048-token prefill")
         result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng)
     if not args.no_cpu_baseline:

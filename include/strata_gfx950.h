@@ -87,6 +87,20 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
                                         int64_t shared_rows, void* shared_h, void* shared_g, void* shared_u,
                                         void* stream);
 
+/* strata_expert_matvec at one token (each pair's own x, share 1: the down call of a routed layer) with a shared
+ * expert's down in the same launch: shared_out[r] = shared_blocks[r, :] . shared_x, shared_blocks a Q4_K matrix of
+ * shared_rows x cols, shared_x its token (float16, its h), shared_out float16. The routed stack IQ3_S or Q2_0 of
+ * 1536 inputs, x float16; out gets strata_expert_matvec's bits. The launch has pairs * ceil(rows / 128)
+ * workgroups, and each takes 16 of the shared rows: more shared rows than that, another kind or width, or a
+ * routed case that runs faster at two units a wave return STRATA_ERR_SHAPE, and the caller then makes the two
+ * calls apart. No counterpart in the reference, whose MoE block calls the routed
+ * experts and then the shared expert (strata_mlx/fused.py:492-493, each down with its SwiGLU): the routed down
+ * launch's waves take the shared expert's rows among their own, which spares its own launch. */
+int strata_expert_matvec_shared(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                                const uint32_t* idx, int64_t pairs, const void* x, int x_dtype, void* out,
+                                int shared_kind, const void* shared_blocks, int64_t shared_rows, const void* shared_x,
+                                void* shared_out, void* stream);
+
 /* The routed experts of one decode token in one launch: h[p, :] = swiglu(gate[idx[p]] . x, up[idx[p]] . x) rounded
  * as strata_expert_gate_up_swiglu rounds it, then out[p, :] = down[idx[p]] . h[p, :]; the same bits as those two
  * calls (strata_expert_gate_up_swiglu, then strata_expert_matvec on down). gate, up (experts, ffn, hidden) and down

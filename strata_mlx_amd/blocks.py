@@ -181,6 +181,39 @@ def gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: tor
     return (g, u, h, sh, *sgu) if with_shared_gu else (g, u, h, sh)
 
 
+def expert_matvec_shared(lin: BlockSwitchLinear, idx: torch.Tensor, shared):
+    """The down call of one token's routed experts, out[pair] = W[idx[pair]] . x[pair] (x (pairs, in), each pair
+    its own h), with a shared expert's down (a layer of the file's Q4_K blocks with `blocks`, `kind`,
+    `output_dims`, `input_dims`: dense.BlockLinear) of its token shared_x (1, in) in the same launch: (out of
+    the pairs, the shared expert's (1, shared rows)), called as f(x, shared_x). None where the launch does not
+    take the case (other types, inputs other than 1536): the caller then makes the two calls apart. The routed
+    and shared experts' down calls of strata_mlx/fused.py:492-493."""
+    if getattr(shared, "blocks", None) is None or getattr(shared, "to_file", None) is not None:
+        raise ValueError("the shared expert's layer as the file's blocks, inputs in the file's order")
+    if shared.input_dims != lin.input_dims:
+        raise ValueError("the shared expert's down takes the routed down's input width")
+
+    def call(x: torch.Tensor, shared_x: torch.Tensor):
+        pairs = idx.numel()
+        x2 = x.reshape(-1, lin.input_dims).contiguous()
+        s2 = shared_x.reshape(-1, shared.input_dims).contiguous()
+        if x2.shape[0] != pairs or s2.shape[0] != 1 or s2.dtype != x2.dtype:
+            return None
+        out = torch.empty((pairs, lin.output_dims), dtype=x.dtype, device=x.device)
+        s_out = torch.empty((1, shared.output_dims), dtype=x.dtype, device=x.device)
+        ix = _idx32(idx)
+        rc = _lib.library().strata_expert_matvec_shared(
+            _lib.kind_id(lin.kind), lin.blocks.data_ptr(), lin.num_experts, lin.output_dims, lin.input_dims,
+            ix.data_ptr(), pairs, x2.data_ptr(), _lib.dtype_id(x.dtype), out.data_ptr(), _lib.kind_id(shared.kind),
+            shared.blocks.data_ptr(), shared.output_dims, s2.data_ptr(), s_out.data_ptr(), _lib.stream())
+        if rc in (_lib.ERR_SHAPE, _lib.ERR_DTYPE, _lib.ERR_KIND):
+            return None
+        _lib.check(rc, f"down with the shared expert {lin.kind} + {shared.kind}")
+        return out, s_out
+
+    return call
+
+
 LAYER_SPIN = 100000  # polls of memory (about a microsecond each) before a wait of expert_layer gives up
 _layer_workspaces = {}
 

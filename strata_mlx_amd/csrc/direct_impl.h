@@ -1357,6 +1357,9 @@ int launch_matvec_any(MatvecParams& p, int x_dtype, int out_dtype, bool glu, int
   if (p.shared[0] != nullptr) {
     if (!glu && x_dtype == DT_F16 && out_dtype == DT_F16 && grid_z == 2 && routed_glu_takes<KIND>(p))
       return launch_routed_glu<KIND>(p, s);
+    if (!glu && x_dtype == DT_F16 && out_dtype == DT_F16 && grid_z == 1 && p.shared_x != nullptr &&
+        routed_down_takes<KIND>(p))
+      return launch_routed_down<KIND>(p, s);
     return STRATA_ERR_SHAPE;
   }
   // a float32 token against Q4_K rows of 4096 inputs: the persistent form, the token in two float16 parts

@@ -144,7 +144,7 @@ int expert_common(int kind, const void* a, const void* b, int64_t experts, int64
 
 extern "C" {
 
-int strata_abi_version(void) { return 3; }
+int strata_abi_version(void) { return 4; }
 
 int strata_block_info(int kind, int* per_block, int* block_bytes) {
   return strata_kind_info(kind, per_block, block_bytes) ? STRATA_ERR_KIND : STRATA_OK;
@@ -229,6 +229,41 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
   p.shared_rows = (int)shared_rows;
   p.shared_row_bytes = s_row_bytes;
   return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 2, (hipStream_t)stream);
+}
+
+int strata_expert_matvec_shared(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,
+                                const uint32_t* idx, int64_t pairs, const void* x, int x_dtype, void* out,
+                                int shared_kind, const void* shared_blocks, int64_t shared_rows, const void* shared_x,
+                                void* shared_out, void* stream) {
+  MatvecParams p = {};
+  int rc = block_shape(kind, rows, cols, &p.row_bytes);
+  if (rc) return rc;
+  int s_row_bytes = 0;
+  rc = block_shape(shared_kind, shared_rows, cols, &s_row_bytes);
+  if (rc) return rc;
+  if (x_dtype != DT_F16) return STRATA_ERR_DTYPE;
+  if (pairs < 1 || experts < 1 || experts > INT32_MAX || shared_rows < 1) return STRATA_ERR_ARG;
+  if (rows == 0) return STRATA_ERR_SHAPE;  // no routed launch to carry the shared expert: the two calls apart
+  if (!blocks || !idx || !x || !out || !shared_blocks || !shared_x || !shared_out) return STRATA_ERR_ARG;
+  if (shared_kind != K_Q4_K || pairs > 65535 || shared_rows > INT32_MAX / 2) return STRATA_ERR_SHAPE;
+  p.blocks[0] = (const uint8_t*)blocks;
+  p.out[0] = out;
+  p.idx = idx;
+  p.x = x;
+  p.mat_bytes = rows * (int64_t)p.row_bytes;
+  p.experts = experts;
+  p.src_rows = (int)rows;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.pairs = (int)pairs;
+  p.share = 1;  // each pair its own token (its h)
+  p.mode = MODE_EXPERT;
+  p.shared[0] = (const uint8_t*)shared_blocks;
+  p.shared_x = shared_x;
+  p.shared_out = shared_out;
+  p.shared_rows = (int)shared_rows;
+  p.shared_row_bytes = s_row_bytes;
+  return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 1, (hipStream_t)stream);
 }
 
 int strata_expert_matvec_swiglu(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,

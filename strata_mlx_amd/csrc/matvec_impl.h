@@ -49,6 +49,7 @@ struct MatvecParams {
   const uint8_t* shared[2];
   void* shared_out;
   void* shared_gu[2];  // the shared expert's gate . x and up . x, or null
+  const void* shared_x;  // the shared expert's token in the routed down launch (its h)
   int shared_rows, shared_row_bytes;
 };
 

@@ -596,70 +596,138 @@ struct DownParams {
   uint32_t experts;
   int rows, row_bytes, pairs, share;
   int groups_per_pair;  // workgroups a pair
+  // the shared expert's down in the same launch (one token, routed_down_kernel's SHARED form): its Q4_K rows
+  // (s_rows x 512 S), its token (512 S float16) and its product out; its unit u (rows 8 u .. 8 u + 7) is taken by
+  // wave u % 2 of workgroup u / 2
+  const uint8_t* s_blocks;
+  const f16* s_x;
+  f16* s_out;
+  int s_rows, s_row_bytes;
 };
 
-template <int KIND, int S, int UPW>
+// SHARED: the shared expert's down in the same launch, one token. Of a workgroup's sixteen waves, waves 0 and 1
+// take a unit of the shared expert's rows each (and no routed unit), waves 2 and 3 two routed units each, and the
+// others one: the same sixteen routed units a workgroup, and no wave holds two types' rows (one with both held
+// its shared rows' fields through the routed decode and spilled 60 registers). At eight pairs of 4096 rows the
+// 256 workgroups take 4096 shared rows: the routed launch alone 8.41 us a layer, with the shared down 8.74 us,
+// the two launches apart 13.19 us.
+template <int KIND, int S, int UPW, bool SHARED = false>
 __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams p) {
   typedef Routed<KIND> R;
+  typedef Routed<K_Q4_K> RS;
   constexpr int kPairs = 8 * S;        // run pairs of a row
   constexpr int kPieces = 8 * kPairs;  // 16-byte pieces of a token
+  static_assert(!SHARED || UPW == 1, "the shared form: sixteen routed units a workgroup");
   __shared__ u32x2 tab[R::kEntries];
   __shared__ u32x4 xs[kPieces];
+  __shared__ u32x4 xs2[SHARED ? kPieces : 1];  // the shared expert's token
   const int tid = threadIdx.x, lane = tid & 63, m = lane & 7, sub = lane >> 3;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int pair = blockIdx.x / p.groups_per_pair, chunk = blockIdx.x - pair * p.groups_per_pair;
 
-  // the table entry this thread expands and a piece of the pair's token, asked for first
+  // the table entry this thread expands and a piece of the pair's token (and of the shared expert's), asked for first
   const uint64_t entry = R::fetch(tid);
   const u32x4 xpiece = reinterpret_cast<const u32x4*>(p.x + (int64_t)(pair / p.share) * (8 * kPieces))[tid % kPieces];
+  u32x4 spiece;
+  if constexpr (SHARED) spiece = reinterpret_cast<const u32x4*>(p.s_x)[tid % kPieces];
   const uint32_t e = p.idx[pair];
   const bool bad = e >= p.experts;
   const uint8_t* mat = p.blocks + (int64_t)(bad ? 0u : e) * p.mat_bytes;
-  int r0[UPW];
-#pragma unroll
-  for (int k = 0; k < UPW; ++k) r0[k] = ((chunk * kGluWaves + wave) * UPW + k) * 8;  // the unit's first row
   R::fill(tab, tid, entry);
   {
     const int c = tid % kPieces;  // threads past the token's pieces write the same bytes again
     xs[glu_x_slot(c >> 3, c & 7)] = xpiece;
+    if constexpr (SHARED) xs2[glu_x_slot(c >> 3, c & 7)] = spiece;
   }
   __syncthreads();
 
-  typename R::Fields f[UPW][S];
+  // N routed units from unit u0 of the pair (rows 8 u0 ..): their rows asked for at once, then each decoded
+  auto routed = [&](auto n_units, int u0) {
+    constexpr int N = decltype(n_units)::value;
+    int r0[N];
 #pragma unroll
-  for (int k = 0; k < UPW; ++k) {
-    const int rl = min(r0[k] + sub, p.rows - 1);  // rows past the matrix read its last row, and write nothing
-    const uint8_t* row = mat + (int64_t)rl * p.row_bytes;
+    for (int k = 0; k < N; ++k) r0[k] = (u0 + k) * 8;  // the unit's first row
+    typename R::Fields f[N][S];
 #pragma unroll
-    for (int st = 0; st < S; ++st) R::load(row, 8 * st + m, f[k][st]);
-    asm volatile("" ::: "memory");
-  }
+    for (int k = 0; k < N; ++k) {
+      const int rl = min(r0[k] + sub, p.rows - 1);  // rows past the matrix read its last row, and write nothing
+      const uint8_t* row = mat + (int64_t)rl * p.row_bytes;
 #pragma unroll
-  for (int k = 0; k < UPW; ++k) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int st = 0; st < S; ++st) {
-      opaque(f[k][st]);
-      const int j = 8 * st + m;
-      uint32_t x[32];
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const u32x4 c = xs[glu_x_slot(j, v)];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
-      }
-      float xsum[2 * kXSums<KIND> + 1];
-      if constexpr (kBiasedRuns<KIND>) {
-        x_sums<KIND>(x, xsum);
-        x_sums<KIND>(x + 16, xsum + kXSums<KIND>);
-      }
-      acc += R::pair_sum_lds(f[k][st], j, x, xsum, tab);
+      for (int st = 0; st < S; ++st) R::load(row, 8 * st + m, f[k][st]);
+      asm volatile("" ::: "memory");
     }
-    acc += lanes_apart(acc, 1);
-    acc += lanes_apart(acc, 2);
-    acc += lanes_apart(acc, 4);
-    const int r = r0[k] + sub;
-    if (m == 0 && r < p.rows) p.out[(int64_t)pair * p.rows + r] = bad ? (f16)__builtin_nanf("") : from_f32<f16>(acc);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        opaque(f[k][st]);
+        const int j = 8 * st + m;
+        uint32_t x[32];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const u32x4 c = xs[glu_x_slot(j, v)];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
+        }
+        float xsum[2 * kXSums<KIND> + 1];
+        if constexpr (kBiasedRuns<KIND>) {
+          x_sums<KIND>(x, xsum);
+          x_sums<KIND>(x + 16, xsum + kXSums<KIND>);
+        }
+        acc += R::pair_sum_lds(f[k][st], j, x, xsum, tab);
+      }
+      acc += lanes_apart(acc, 1);
+      acc += lanes_apart(acc, 2);
+      acc += lanes_apart(acc, 4);
+      const int r = r0[k] + sub;
+      if (m == 0 && r < p.rows)
+        p.out[(int64_t)pair * p.rows + r] = bad ? (f16)__builtin_nanf("") : from_f32<f16>(acc);
+    }
+  };
+
+  if constexpr (!SHARED) {
+    routed(std::integral_constant<int, UPW>(), (chunk * kGluWaves + wave) * UPW);
+  } else {
+    const int u = chunk * kGluWaves;  // the workgroup's first routed unit
+    if (wave >= 4) {
+      routed(std::integral_constant<int, 1>(), u + wave);
+    } else if (wave >= 2) {
+      routed(std::integral_constant<int, 2>(), u + 2 * (wave - 2));
+    } else {
+      const int s_unit = 2 * blockIdx.x + wave;  // rows 8 s_unit .. of the shared expert's down
+      if (8 * s_unit < p.s_rows) {
+        typename RS::Fields fs[S];
+        const int rl = min(s_unit * 8 + sub, p.s_rows - 1);
+        const uint8_t* row = p.s_blocks + (int64_t)rl * p.s_row_bytes;
+#pragma unroll
+        for (int st = 0; st < S; ++st) RS::load(row, 8 * st + m, fs[st]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+          opaque(fs[st]);
+          const int j = 8 * st + m;
+          int jx = j;  // read after the last run pair's sum: the token's 32 registers held for one run pair at a time
+          asm volatile("" : "+v"(jx) : "v"(acc));
+          uint32_t x[32];
+#pragma unroll
+          for (int v = 0; v < 8; ++v) {
+            const u32x4 c = xs2[glu_x_slot(jx, v)];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[4 * v + i] = c[i];
+          }
+          float xsum[2 * kXSums<K_Q4_K> + 1];
+          x_sums<K_Q4_K>(x, xsum);
+          x_sums<K_Q4_K>(x + 16, xsum + kXSums<K_Q4_K>);
+          acc += RS::pair_sum(fs[st], j, x, xsum, tab);
+        }
+        acc += lanes_apart(acc, 1);
+        acc += lanes_apart(acc, 2);
+        acc += lanes_apart(acc, 4);
+        const int r = s_unit * 8 + sub;
+        if (m == 0 && r < p.s_rows) p.s_out[r] = from_f32<f16>(acc);
+      }
+    }
   }
 }
 
@@ -674,13 +742,14 @@ bool routed_down_takes(const MatvecParams& p) {
          p.glu_out == nullptr && p.experts <= INT32_MAX && p.pairs <= 65535;
 }
 
-template <int KIND, int S, int UPW>
+template <int KIND, int S, int UPW, bool SHARED = false>
 int launch_down_su(DownParams& p, int units_per_pair, hipStream_t s) {
   const int per_group = kGluWaves * UPW;
   p.groups_per_pair = (units_per_pair + per_group - 1) / per_group;
   const int64_t groups = (int64_t)p.groups_per_pair * p.pairs;
   if (groups > INT32_MAX) return STRATA_ERR_SHAPE;
-  hipLaunchKernelGGL((routed_down_kernel<KIND, S, UPW>), dim3((unsigned)groups), dim3(kGluThreads), 0, s, p);
+  if (SHARED && (p.s_rows + 7) / 8 > 2 * groups) return STRATA_ERR_SHAPE;  // two shared units a workgroup
+  hipLaunchKernelGGL((routed_down_kernel<KIND, S, UPW, SHARED>), dim3((unsigned)groups), dim3(kGluThreads), 0, s, p);
   STRATA_CHECK_LAUNCH();
   return STRATA_OK;
 }
@@ -710,6 +779,15 @@ int launch_routed_down(const MatvecParams& mp, hipStream_t s) {
       return (groups + cus - 1) / cus * upw;
     };
     const bool two = cost(2) < cost(1);
+    if (mp.shared[0] != nullptr) {  // the shared expert's down in the launch: rows of 1536 inputs, one unit a wave
+      p.s_blocks = mp.shared[0];
+      p.s_x = reinterpret_cast<const f16*>(mp.shared_x);
+      p.s_out = reinterpret_cast<f16*>(mp.shared_out);
+      p.s_rows = mp.shared_rows;
+      p.s_row_bytes = mp.shared_row_bytes;
+      if (mp.cols != 1536 || two) return STRATA_ERR_SHAPE;
+      return launch_down_su<KIND, 3, 1, true>(p, units_per_pair, s);
+    }
     if (mp.cols == 1536)
       return two ? launch_down_su<KIND, 3, 2>(p, units_per_pair, s) : launch_down_su<KIND, 3, 1>(p, units_per_pair, s);
     return two ? launch_down_su<KIND, 5, 2>(p, units_per_pair, s) : launch_down_su<KIND, 5, 1>(p, units_per_pair, s);

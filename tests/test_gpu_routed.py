@@ -262,3 +262,47 @@ def test_gate_up_with_shared_expert(gpu, kind, pairs, rows, s_rows):
     assert rel_l2(sh.float().cpu().numpy()[0], want) <= 2e-3
     _, _, hd = D.gate_up_swiglu(sg, su, xs)
     assert rel_l2(sh.float().cpu().numpy()[0], hd.float().cpu().numpy()[0]) <= 2e-3
+
+
+# the shared expert's down (Q4_K rows of 1536 inputs) in the routed down launch at one token: the routed outputs
+# are the plain launch's bits (NaN for the pair naming no expert), the shared rows at 1e-3 of the oracle's float64
+# product (strata_mlx/fused.py:492-493); cases the launch does not take (inputs of 2560, more shared rows than two
+# units a workgroup cover) return None
+@pytest.mark.parametrize("kind,pairs,rows,cols,s_rows", [("IQ3_S", 8, 4096, 1536, 4096), ("Q2_0", 8, 4096, 1536, 4096),
+                                                         ("IQ3_S", 3, 200, 1536, 90), ("Q2_0", 1, 4096, 1536, 500),
+                                                         ("IQ3_S", 3, 200, 1536, 100), ("IQ3_S", 4, 512, 2560, 64)])
+def test_down_with_shared_expert(gpu, kind, pairs, rows, cols, s_rows):
+    from strata_mlx_amd import dense as D
+    experts = 10
+    g = torch.Generator(device=gpu).manual_seed(pairs * 10 + s_rows)
+    lin = B.BlockSwitchLinear(synth.random_stack(kind, experts * rows * cols, gpu, g), kind, (experts, rows, cols))
+    sd = D.BlockLinear(synth.random_stack("Q4_K", s_rows * cols, gpu, g), "Q4_K", (s_rows, cols))
+    rng = np.random.default_rng(rows + s_rows)
+    idx = rng.choice(experts, pairs, replace=False).astype(np.int32)
+    if pairs >= 3:
+        idx[1] = experts + 2  # names no expert
+    x = (rng.standard_normal((pairs, cols)) / 8).astype(np.float16)
+    sx = (rng.standard_normal((1, cols)) / 8).astype(np.float16)
+    xs, ix, sxs = torch.from_numpy(x).to(gpu), torch.from_numpy(idx).to(gpu), torch.from_numpy(sx).to(gpu)
+    got = B.expert_matvec_shared(lin, ix, sd)(xs, sxs)
+    groups = pairs * -(-rows // 128)  # sixteen units of eight rows a workgroup
+    if cols != 1536 or -(-s_rows // 8) > 2 * groups:
+        assert got is None
+        return
+    y, sy = got
+    torch.cuda.synchronize()
+    plain = B.expert_matvec(lin, ix, xs)
+    assert torch.equal(y.view(torch.int16), plain.view(torch.int16))
+    if pairs >= 3:
+        assert torch.isnan(y[1]).all()
+    want = O.dequantize(sd.blocks.cpu().numpy(), "Q4_K", (s_rows, cols)).astype(np.float64) @ sx[0].astype(np.float64)
+    assert rel_l2(sy.float().cpu().numpy()[0], want) <= REL
+    # calls with another shared token, then the first again: nothing carried from one call to the next
+    call = B.expert_matvec_shared(lin, ix, sd)
+    y2, sy2 = call(xs, -sxs)
+    y3, sy3 = call(xs, sxs)
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(torch.int16), plain.view(torch.int16))
+    assert rel_l2(sy2.float().cpu().numpy()[0], -want) <= REL
+    assert torch.equal(y3.view(torch.int16), plain.view(torch.int16))
+    assert torch.equal(sy3.view(torch.int16), sy.view(torch.int16))
