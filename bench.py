@@ -582,6 +582,15 @@ def main():
         note("shared expert's down in the routed down launch")
         result["dense_decode"]["shared_down_in_routed"] = shared_down_bench(B, D, synth, dev, lins, args.steps,
                                                                             args.warmup, rng)
+        # the same token with the shared expert's launches replaced by their marginal cost in the routed launches
+        lay, sg, sd = dd["layers"], result["dense_decode"]["shared_in_routed"], result["dense_decode"]["shared_down_in_routed"]
+        riding_us = sum(lay[n]["us"] for n in ("qkv", "o", "lm_head")) + max(0.0, sg["shared_marginal_us"]) + \
+            max(0.0, sd["shared_marginal_us"])
+        result["dense_decode"]["shared_riding"] = {
+            "us_per_token": round(riding_us, 1), "gbs": round(dd["bytes_per_token"] / riding_us / 1e3, 1),
+            "hbm_frac": round(dd["bytes_per_token"] / riding_us / 1e3 / HBM_PEAK_GBS, 4),
+            "note": "q/k/v, o and lm_head as above; the shared expert's gate/up and down at their marginal time in "
+                    "the routed launches (the same bytes a token)"}
         note("2048-token prefill")
         result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng)
     if not args.no_cpu_baseline:

@@ -609,8 +609,8 @@ struct DownParams {
 // take a unit of the shared expert's rows each (and no routed unit), waves 2 and 3 two routed units each, and the
 // others one: the same sixteen routed units a workgroup, and no wave holds two types' rows (one with both held
 // its shared rows' fields through the routed decode and spilled 60 registers). At eight pairs of 4096 rows the
-// 256 workgroups take 4096 shared rows: the routed launch alone 8.41 us a layer, with the shared down 8.74 us,
-// the two launches apart 13.19 us.
+// 256 workgroups take 4096 shared rows: the routed launch alone 8.4 us a layer, with the shared down 8.7-9.1 us,
+// the two launches apart 13.2 us.
 template <int KIND, int S, int UPW, bool SHARED = false>
 __global__ __launch_bounds__(kGluThreads, 4) void routed_down_kernel(DownParams p) {
   typedef Routed<KIND> R;
