@@ -82,3 +82,26 @@ def test_arguments_are_checked_before_any_launch():
         _lib.check(_lib.ERR_SHAPE, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.ERR_LAUNCH, "x")
+
+
+def test_shared_expert_entry_points_check_their_arguments():
+    lib = _lib.library()
+    q, k4 = _lib.kind_id("IQ3_S"), _lib.kind_id("Q4_K")
+    gs = lib.strata_expert_gate_up_swiglu_shared
+    #        kind gate up experts rows cols idx pairs x  dtype g  u  h  s_kind s_gate s_up s_rows s_h s_g s_u stream
+    assert gs(q, 1, 1, 4, 1536, 4096, 1, 8, 1, 0, 1, 1, 1, k4, 1, 1, 1536, 1, None, None, None) == _lib.ERR_DTYPE
+    assert gs(q, 1, 1, 4, 1536, 4096, 1, 8, 1, 1, 1, 1, 1, q, 1, 1, 1536, 1, None, None, None) == _lib.ERR_SHAPE
+    assert gs(q, 1, 1, 4, 1536, 4096, 1, 8, 1, 1, 1, 1, 1, k4, 0, 1, 1536, 1, None, None, None) == _lib.ERR_ARG
+    assert gs(q, 1, 1, 4, 0, 4096, 1, 8, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, None, None, None) == _lib.ERR_SHAPE
+    assert gs(q, 1, 1, 4, 1536, 4000, 1, 8, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, None, None, None) == _lib.ERR_SHAPE
+    ms = lib.strata_expert_matvec_shared
+    #        kind blocks experts rows cols idx pairs x dtype out s_kind s_blocks s_rows s_x s_out stream
+    assert ms(q, 1, 4, 4096, 1536, 1, 8, 1, 0, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_DTYPE  # float32 h
+    assert ms(q, 1, 4, 4096, 1536, 1, 8, 1, 1, 1, q, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # shared not Q4_K
+    assert ms(q, 1, 4, 4096, 1536, 1, 8, 1, 1, 1, k4, 1, 4096, 0, 1, None) == _lib.ERR_ARG  # null shared token
+    assert ms(q, 1, 4, 4096, 1536, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 0, None) == _lib.ERR_ARG  # null shared out
+    assert ms(q, 1, 4, 4096, 1536, 1, 0, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_ARG  # no pairs
+    assert ms(q, 1, 4, 0, 1536, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # no routed rows
+    assert ms(q, 1, 4, 4096, 1536, 1, 70000, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # > 65535 pairs
+    assert ms(q, 1, 4, 4096, 1500, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # not whole blocks
+    assert ms(99, 1, 4, 4096, 1536, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_KIND
