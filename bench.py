@@ -487,8 +487,8 @@ def prefill_bench(B, D, synth, dev, lins, steps, warmup, rng, tokens=2048):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
-              "see DESIGN.md for how the path would shard", file=sys.stderr)
+        print(f"bench.py runs on one GPU: the path has no multi-GPU form (asked for {args.gpus} GPUs); "
+              "it measures one GPU's share", file=sys.stderr)
         sys.exit(2)
     from strata_mlx_amd import blocks as B
     from strata_mlx_amd import synth

@@ -26,7 +26,7 @@ BLOCK = {"IQ4_NL": (32, 18), "IQ4_XS": (256, 136), "IQ3_S": (256, 110), "IQ3_XXS
 # the dense types of the loader, decoded by the same kernels (strata_mlx/gguf.py:25-33)
 DENSE = {"Q4_0": (32, 18), "Q5_0": (32, 22), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q5_K": (256, 176),
          "Q6_K": (256, 210)}
-# the codebooks of these were not available to this build: the kernels refuse them
+# these types' codebooks are not in the package (no source of them to pin against): the kernels refuse them
 NO_GRID = ("IQ2_S", "IQ2_XS", "IQ2_XXS", "IQ1_M")
 
 TOKENS_TILE = 16  # slots of a tile (strata_mlx/blocks.py:581)

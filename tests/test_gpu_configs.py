@@ -258,9 +258,9 @@ def test_prompt_chunk_as_benchmarked(gpu):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_prompt_chunk_in_q2_0(gpu, dtype):
-    """Config 4's shape in Q2_0 (the prompt target of the north star names IQ3_S and Q2_0): 512 tokens, 256 experts
-    top-8 of Zipf routing, gate/up 1536 x 4096 and down 4096 x 1536, through switch_glu's tiles (the fused gate/up
-    SwiGLU and scatter-down kernels on Q2_0's unstaged field loads), bfloat16 and float16."""
+    """Config 4's shape in Q2_0 (the prompt-chunk target is stated for IQ3_S and Q2_0 blocks): 512 tokens, 256
+    experts top-8 of Zipf routing, gate/up 1536 x 4096 and down 4096 x 1536, through switch_glu's tiles (the fused
+    gate/up SwiGLU and scatter-down kernels on Q2_0's rows staged in LDS), bfloat16 and float16."""
     layer = {n: Stack("Q2_0", E, r, c, 520 + i, gpu) for i, (n, (r, c)) in
              enumerate((("gate", (F, H)), ("up", (F, H)), ("down", (H, F))))}
     prompt_check(gpu, layer, "Q2_0", 512, dtype, 14)
