@@ -8,7 +8,8 @@ reference's call surface with torch tensors on the GPU:
              gate_up_swiglu, tiles_of, tile_matmul, switch_glu          (strata_mlx/blocks.py)
     dense    ScaledLinear, BlockLinear, BlockEmbedding                  (strata_mlx/dense.py)
     rows     rows_of: listed rows of an output layer, read in place     (strata_mlx/rows.py)
-    fused    WindowLinear (the router), top_k, moe_combine, route       (strata_mlx/fused.py)
+    fused    WindowLinear (the router), top_k, moe_combine, route,
+             RoutedMoE (the MoE block)                                  (strata_mlx/fused.py)
     gguf     GGUF, shards, upload, experts, linear, embedding           (strata_mlx/gguf.py, load.py)
     synth    synthetic blocks and Zipf routing for benchmarks and tests
 """

@@ -5,6 +5,8 @@ with torch tensors on the GPU in place of mx.array.
     top_k         the k largest logits of each row, ties to the lower index; with `weights`, their softmax
     moe_combine   sum_k y_k * w_k plus sigmoid(g) * the shared expert, in the reference's order and rounding
     route         router -> top_k -> softmax, as _Routed.__call__ makes the experts' indices and weights
+    RoutedMoE     the whole MoE block of _Routed.__call__: route, the routed experts, the shared expert and its
+                  gate, moe_combine; at one token the shared expert rides in the routed launches
 """
 
 import torch
@@ -80,3 +82,63 @@ def route(router: WindowLinear, x: torch.Tensor, k: int):
     strata_mlx/fused.py:488-491 makes them."""
     logits = router(x)
     return top_k(logits, k, weights=True)
+
+
+class RoutedMoE:
+    """The model's MoE block with the router's choice made by `top_k` and its end by `moe_combine`
+    (strata_mlx/fused.py:484-497, `_Routed.__call__`): the router's logits, the top_k experts and the softmax of
+    their logits (`route`); y = the routed experts (`switch`, a blocks.BlockSwitchGLU); g = shared_expert_gate(x) (a
+    WindowLinear of one row); s = the shared expert, down . swiglu(gate . x, up . x) (dense.BlockLinear layers of the
+    file's blocks); then moe_combine(y, w, g, s), or where it declines, sum_k y_k * w_k in float32 rounded to x's
+    type, plus sigmoid(g) * s, in float32 as MLX promotes it.
+
+    At one token the shared expert's gate and up ride in the routed gate/up launch and its down in the routed down
+    launch (blocks.gate_up_swiglu_shared, blocks.expert_matvec_shared), where those take the case; elsewhere, and
+    where they decline, the routed experts and the shared expert run apart. `last_path` says which ran."""
+
+    def __init__(self, router: WindowLinear, switch, shared_gate, shared_up, shared_down,
+                 shared_expert_gate: WindowLinear, k: int):
+        self.router, self.switch, self.k = router, switch, k
+        self.shared_gate, self.shared_up, self.shared_down = shared_gate, shared_up, shared_down
+        self.shared_expert_gate = shared_expert_gate
+        self.last_path = None
+
+    def shared_expert(self, x: torch.Tensor) -> torch.Tensor:
+        """down . swiglu(gate . x, up . x) of the shared expert, its own launches: (tokens, hidden)."""
+        from . import dense
+        _, _, h = dense.gate_up_swiglu(self.shared_gate, self.shared_up, x)
+        return self.shared_down(h)
+
+    def _riding(self, x: torch.Tensor, idx: torch.Tensor):
+        """(y (1, k, hidden), s (1, hidden)) with the shared expert in the routed launches, or None."""
+        from . import blocks
+        sw = self.switch
+        flat = idx.reshape(-1)
+        r = blocks.gate_up_swiglu_shared(sw.gate_proj, sw.up_proj, x, flat, self.shared_gate, self.shared_up)
+        if r is None:
+            return None
+        _, _, h, sh = r
+        both = blocks.expert_matvec_shared(sw.down_proj, flat, self.shared_down)(h, sh)
+        if both is None:  # the down launch does not take it: the shared down on its own launch
+            y, s = blocks.expert_matvec(sw.down_proj, flat, h), self.shared_down(sh)
+            self.last_path = "gate/up riding"
+        else:
+            y, s = both
+            self.last_path = "riding"
+        return y.reshape(1, self.k, -1), s
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        lead, hidden = x.shape[:-1], x.shape[-1]
+        x2 = x.reshape(-1, hidden)
+        idx, w = route(self.router, x2, self.k)
+        g = self.shared_expert_gate(x2)
+        both = self._riding(x2, idx) if x2.shape[0] == 1 else None
+        if both is None:
+            y, s = self.switch(x2, idx).reshape(x2.shape[0], self.k, -1), self.shared_expert(x2)
+            self.last_path = "apart"
+        else:
+            y, s = both
+        out = moe_combine(y, w, g, s)
+        if out is None:
+            out = (y.float() * w[..., None]).sum(dim=-2).to(x.dtype).float() + torch.sigmoid(g.float()) * s.float()
+        return out.reshape(*lead, -1)

@@ -70,3 +70,56 @@ def test_route_gives_experts_and_weights_of_the_router(gpu):
     # a near-tie between float32 sums may order two experts differently; the chosen set is the oracle's
     assert all(set(a) == set(b) for a, b in zip(idx.cpu().numpy(), want))
     assert np.allclose(wts.sum(dim=-1).cpu().numpy(), 1.0, atol=1e-6)
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return np.linalg.norm(got - want) / np.linalg.norm(want)
+
+
+# The whole MoE block (strata_mlx/fused.py:484-497): router, top-k, IQ3_S routed experts (SwitchGLU), a Q4_K shared
+# expert and its sigmoid gate, the combine; at one token with the shared expert in the routed launches, at two
+# apart. Against the oracle's chain on the library's own choice of experts (checked above): float64 products of
+# the oracle's weights, h as mlx-lm's SwiGLU rounds it, y and s rounded to float16, the reference's combine, within
+# 2e-3 relative L2 (an h on the other side of a rounding boundary moves a few elements by a float16 step).
+@pytest.mark.parametrize("tokens", [1, 2])
+def test_moe_block_against_the_oracle(gpu, tokens):
+    from oracle import blocks as O
+    from strata_mlx_amd import blocks as B
+    from strata_mlx_amd import dense as D
+    from strata_mlx_amd import synth
+    H, F, E, K = 4096, 1536, 10, 8
+    g = torch.Generator(device=gpu).manual_seed(41 + tokens)
+    shapes = ((F, H), (F, H), (H, F))
+    stacks = [synth.random_stack("IQ3_S", E * r * c, gpu, g) for r, c in shapes]
+    switch = B.BlockSwitchGLU(*(B.BlockSwitchLinear(st, "IQ3_S", (E, r, c)) for st, (r, c) in zip(stacks, shapes)))
+    shared = [D.BlockLinear(synth.random_stack("Q4_K", r * c, gpu, g), "Q4_K", (r, c)) for r, c in shapes]
+    rng = np.random.default_rng(tokens)
+    rw = (rng.standard_normal((E, H)) / 64).astype(np.float16)
+    gw = (rng.standard_normal((1, H)) / 64).astype(np.float16)
+    router = FU.WindowLinear(torch.from_numpy(rw).to(gpu))
+    moe = FU.RoutedMoE(router, switch, *shared, FU.WindowLinear(torch.from_numpy(gw).to(gpu)), K)
+    x = (rng.standard_normal((tokens, H)) / 64).astype(np.float16)
+    xs = torch.from_numpy(x).to(gpu)
+    out = moe(xs)
+    assert out.shape == (tokens, H) and out.dtype == torch.float16
+    assert moe.last_path == ("riding" if tokens == 1 else "apart")
+    idx_t, w_t = FU.route(router, xs, K)
+    idx, w = idx_t.cpu().numpy(), w_t.cpu().numpy()
+    got = out.float().cpu().numpy()
+
+    xd = x.astype(np.float64)
+    raw = [st.cpu().numpy().reshape(E, -1) for st in stacks]
+    y = np.zeros((tokens, K, H), np.float16)
+    for e in np.unique(idx):
+        gate, up, down = (O.dequantize(raw[i][e], "IQ3_S", shapes[i]).astype(np.float64) for i in range(3))
+        for t, j in zip(*np.nonzero(idx == e)):
+            h = O.swiglu_rounded(gate @ xd[t], up @ xd[t], np.float16).astype(np.float64)
+            y[t, j] = (down @ h).astype(np.float16)
+    sgw, suw, sdw = (O.dequantize(lay.blocks.cpu().numpy(), "Q4_K", (lay.output_dims, lay.input_dims))
+                     .astype(np.float64) for lay in shared)
+    sh = O.swiglu_rounded(xd @ sgw.T, xd @ suw.T, np.float16).astype(np.float64)
+    s = (sh @ sdw.T).astype(np.float16)
+    gl = (xd @ gw.astype(np.float64).T).reshape(tokens).astype(np.float16)
+    want = OF.moe_combine(y, w, gl, s)
+    assert rel_l2(got, want) <= 2e-3
