@@ -22,6 +22,8 @@ Beside it, on the same line, the other workloads of the path:
                  1 GB a graph); shared_in_routed: the shared expert's gate and up taken by the headline layers'
                  routed gate+up launches instead (its marginal time over those launches alone);
                  shared_down_in_routed: its down taken by the layers' routed down launches the same way
+  moe_block      one decode token through whole MoE blocks (fused.RoutedMoE: router, top-8, routed experts, the
+                 shared expert riding in the routed launches, its gate, the combine): us a block and GB/s
   prefill        a 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts through the tiles and
                  the dense layers dequantized for the chunk and multiplied by the library product, TFLOPS
   roofline       the dominant kernel (the gate+up+SwiGLU launch): algorithmic bytes per launch / its mean duration
@@ -345,6 +347,55 @@ def shared_down_bench(B, D, synth, dev, lins, steps, warmup, rng):
             "fused_hbm_frac": round((routed_bytes + shared_bytes) / (us["fused"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def moe_block_bench(B, D, FU, synth, dev, lins, steps, warmup):
+    """One decode token through the layers' whole MoE blocks (fused.RoutedMoE: the router (256 x 4096 float16), its
+    top-8 and softmax, the routed IQ3_S experts, a Q4_K shared expert riding in the routed launches, its sigmoid gate,
+    the combine), each block's routing made by its own router from the same token: microseconds a block and the
+    block's bytes (the distinct experts' rows, the shared expert, the router and gate weights) over that time."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(8)
+    x = (torch.randn((1, H), device=dev) / 64).half()
+    blocks, mats = [], []
+    for gate, up, down in lins:
+        router = FU.WindowLinear((torch.randn((E, H), device=dev, generator=g) / 64).half())
+        shared = [D.BlockLinear(synth.random_stack("Q4_K", r * c, dev, g), "Q4_K", (r, c)) for r, c in
+                  ((F, H), (F, H), (H, F))]
+        sgate = FU.WindowLinear((torch.randn((1, H), device=dev, generator=g) / 64).half())
+        blocks.append(FU.RoutedMoE(router, B.BlockSwitchGLU(gate, up, down), *shared, sgate, K))
+        mats.append((router, shared))
+
+    def run():
+        for moe in blocks:
+            moe(x)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    paths = sorted({moe.last_path for moe in blocks})
+    if paths != ["riding"]:
+        raise RuntimeError(f"the shared expert did not ride in the routed launches: {paths}")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    us = time_graph(graph, steps, warmup) / steps / len(blocks) * 1e6
+    distinct = []
+    for moe in blocks:  # each block's experts, as its router chose them for this token
+        idx, _ = FU.route(moe.router, x, K)
+        distinct.append(len(torch.unique(idx)))
+    row = lins[0][0].blocks.numel() // E  # one expert's gate (or up, or down) bytes
+    routed = sum(distinct) / len(distinct) * 3 * row
+    shared_bytes = sum(lay.blocks.numel() for lay in mats[0][1])
+    total = routed + shared_bytes + E * H * 2 + H * 2 + K * F * 2 + H * 2
+    return {"workload": f"one decode token through {len(blocks)} MoE blocks: router 256 x 4096 float16, top-8, "
+                        f"routed IQ3_S {F} x {H} / {H} x {F}, shared expert Q4_K riding in the routed launches, "
+                        f"its gate, the combine", "us_per_block": round(us, 2),
+            "bytes_per_block": int(total), "gbs": round(total / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(total / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def host_cpu():
     """(the host's cores as this process sees them, the threads BLAS is given, the CPU model)."""
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -591,6 +642,9 @@ def main():
             "hbm_frac": round(dd["bytes_per_token"] / riding_us / 1e3 / HBM_PEAK_GBS, 4),
             "note": "q/k/v, o and lm_head as above; the shared expert's gate/up and down at their marginal time in "
                     "the routed launches (the same bytes a token)"}
+        note("whole MoE blocks at one token")
+        from strata_mlx_amd import fused as FU
+        result["moe_block"] = moe_block_bench(B, D, FU, synth, dev, lins, args.steps, args.warmup)
         note("2048-token prefill")
         result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng)
     if not args.no_cpu_baseline:

@@ -235,6 +235,19 @@ int strata_router_matvec(const void* w, int64_t rows, int64_t cols, const void* 
 int strata_top_k(const float* logits, int64_t rows, int64_t n, int64_t k, uint32_t* idx, float* weights,
                  void* stream);
 
+/* strata_router_matvec and strata_top_k in one launch, at 1-8 tokens: logits (tokens, rows) float32 = W . x as
+ * strata_router_matvec gives them; idx (tokens, k) and weights (tokens, k, or NULL) as strata_top_k gives them
+ * over each token's first `experts` logits (experts <= 2048, k <= 64); extra (tokens, rows - experts) float16, or
+ * NULL: the rows past the experts' rounded once (a shared expert's gate, one more row of W). `count` is a uint32
+ * of device memory, zero before the first call, that the launch leaves at zero: the workgroups count themselves
+ * there, and the last to finish its rows makes the choice. Calls that overlap on one `count` race: one a stream.
+ * No single counterpart in the reference, whose MoE block calls the router, top_k and the shared expert's gate
+ * apart (WindowLinear + _MATVEC, top_k + _TOPK, the softmax and shared_expert_gate of _Routed.__call__,
+ * strata_mlx/fused.py:356-390, 400-436, 488-493); tokens past 8 return STRATA_ERR_SHAPE (those calls apart). */
+int strata_router_route(const void* w, int64_t rows, int64_t cols, const void* x, int64_t tokens, int x_dtype,
+                        float* logits, int64_t experts, int64_t k, uint32_t* idx, float* weights, void* extra,
+                        uint32_t* count, void* stream);
+
 /* out[t, :] = half(sum_j y[t, j, :] * w[t, j]) + half(half(sigmoid(g[t])) * s[t, :]): y (rows, k, d),
  * g (rows), s and out (rows, d) float16, w (rows, k) float32. The experts are added in the order of the
  * reference (eight partial sums, expert j into sum j % 8, each product rounded before it is added, then

@@ -144,7 +144,7 @@ int expert_common(int kind, const void* a, const void* b, int64_t experts, int64
 
 extern "C" {
 
-int strata_abi_version(void) { return 4; }
+int strata_abi_version(void) { return 5; }
 
 int strata_block_info(int kind, int* per_block, int* block_bytes) {
   return strata_kind_info(kind, per_block, block_bytes) ? STRATA_ERR_KIND : STRATA_OK;

@@ -84,6 +84,44 @@ def route(router: WindowLinear, x: torch.Tensor, k: int):
     return top_k(logits, k, weights=True)
 
 
+_route_counts = {}
+
+
+def _route_count(device: torch.device) -> torch.Tensor:
+    """The count strata_router_route keeps for one device and stream, zeroed when first made (each launch leaves
+    it at zero)."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    c = _route_counts.get(key)
+    if c is None:
+        c = torch.zeros(1, dtype=torch.int32, device=device)
+        _route_counts[key] = c
+    return c
+
+
+def route_gated(router: WindowLinear, x: torch.Tensor, experts: int, k: int):
+    """route() and the rows of the router's weight past the experts' (a shared expert's gate, stacked under the
+    router's rows) in one launch (strata_router_route): (indices (tokens, k) int32, weights (tokens, k) float32,
+    those rows' products (tokens, rows - experts) float16), or None where the launch does not take the case (more
+    than 8 tokens, a float type other than float16 / float32); the caller then makes the calls apart."""
+    x2 = x.reshape(-1, router.cols).contiguous()
+    tokens = x2.shape[0]
+    if tokens == 0 or tokens > 8 or x2.dtype not in (torch.float16, torch.float32) or router.cols % 8:
+        return None
+    dev = x.device
+    logits = torch.empty((tokens, router.rows), dtype=torch.float32, device=dev)
+    idx = torch.empty((tokens, k), dtype=torch.int32, device=dev)
+    w = torch.empty((tokens, k), dtype=torch.float32, device=dev)
+    nx = router.rows - experts
+    extra = torch.empty((tokens, nx), dtype=torch.float16, device=dev) if nx > 0 else None
+    rc = _lib.library().strata_router_route(router.weight.data_ptr(), router.rows, router.cols, x2.data_ptr(), tokens,
+                                            _lib.dtype_id(x2.dtype), logits.data_ptr(), experts, k, idx.data_ptr(),
+                                            w.data_ptr(), _lib.ptr(extra), _route_count(dev).data_ptr(), _lib.stream())
+    if rc == _lib.ERR_SHAPE:
+        return None
+    _lib.check(rc, "router_route")
+    return idx, w, extra
+
+
 class RoutedMoE:
     """The model's MoE block with the router's choice made by `top_k` and its end by `moe_combine`
     (strata_mlx/fused.py:484-497, `_Routed.__call__`): the router's logits, the top_k experts and the softmax of
@@ -102,6 +140,10 @@ class RoutedMoE:
         self.shared_gate, self.shared_up, self.shared_down = shared_gate, shared_up, shared_down
         self.shared_expert_gate = shared_expert_gate
         self.last_path = None
+        # the router's rows and the shared expert's gate as one weight: its products and the choice in one launch
+        self.stacked = None
+        if shared_expert_gate.cols == router.cols:
+            self.stacked = WindowLinear(torch.cat([router.weight, shared_expert_gate.weight]))
 
     def shared_expert(self, x: torch.Tensor) -> torch.Tensor:
         """down . swiglu(gate . x, up . x) of the shared expert, its own launches: (tokens, hidden)."""
@@ -130,8 +172,12 @@ class RoutedMoE:
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         lead, hidden = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, hidden)
-        idx, w = route(self.router, x2, self.k)
-        g = self.shared_expert_gate(x2)
+        both_gates = route_gated(self.stacked, x2, self.router.rows, self.k) if self.stacked is not None else None
+        if both_gates is None:
+            idx, w = route(self.router, x2, self.k)
+            g = self.shared_expert_gate(x2)
+        else:
+            idx, w, g = both_gates
         both = self._riding(x2, idx) if x2.shape[0] == 1 else None
         if both is None:
             y, s = self.switch(x2, idx).reshape(x2.shape[0], self.k, -1), self.shared_expert(x2)

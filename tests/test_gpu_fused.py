@@ -123,3 +123,50 @@ def test_moe_block_against_the_oracle(gpu, tokens):
     gl = (xd @ gw.astype(np.float64).T).reshape(tokens).astype(np.float16)
     want = OF.moe_combine(y, w, gl, s)
     assert rel_l2(got, want) <= 2e-3
+
+
+# The router's product and the choice in one launch (strata_router_route) against the two launches it replaces:
+# the same experts, the same weights' bits, the rows past the experts (a shared expert's gate) the router's float32
+# sums rounded once to float16; calls in a row and graph replays (the launch's count returns to zero each time).
+@pytest.mark.parametrize("tokens,experts,extra,k", [(1, 256, 1, 8), (3, 256, 0, 8), (8, 100, 3, 7), (5, 64, 1, 64),
+                                                    (2, 2048, 2, 10)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_router_and_choice_in_one_launch(gpu, tokens, experts, extra, k, dtype):
+    rng = np.random.default_rng(tokens * 31 + experts + extra)
+    wt = (rng.standard_normal((experts + extra, 4096)) / 64).astype(np.float16)
+    stacked = FU.WindowLinear(torch.from_numpy(wt).to(gpu))
+    router = FU.WindowLinear(torch.from_numpy(wt[:experts]).to(gpu))
+    xs = [torch.from_numpy(rng.standard_normal((tokens, 4096)).astype(np.float32)).to(dtype).to(gpu) for _ in range(3)]
+
+    def check(got, x):
+        idx, w, ex = got
+        want_idx, want_w = FU.route(router, x, k)
+        assert torch.equal(idx, want_idx)
+        assert torch.equal(w.view(torch.int32), want_w.view(torch.int32))
+        if extra:
+            want_ex = stacked(x)[:, experts:].to(torch.float16)
+            assert torch.equal(ex.view(torch.int16), want_ex.view(torch.int16))
+        else:
+            assert ex is None
+
+    for x in xs:  # calls in a row
+        check(FU.route_gated(stacked, x, experts, k), x)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        FU.route_gated(stacked, xs[0], experts, k)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    x_in = xs[0].clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = FU.route_gated(stacked, x_in, experts, k)
+    for r in range(3):
+        x_in.copy_(xs[r])
+        graph.replay()
+        torch.cuda.synchronize()
+        check(got, xs[r])
+        FU.route_gated(stacked, xs[(r + 1) % 3], experts, k)  # eager work between the replays
+        torch.cuda.synchronize()
+    assert FU.route_gated(stacked, torch.cat([xs[0]] * 9)[:9], experts, k) is None  # 9 tokens: the calls apart

@@ -25,7 +25,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.strata_abi_version() == 4
+    assert lib.strata_abi_version() == 5
 
 
 @pytest.mark.parametrize("kind, per, size", [("Q2_0", 64, 18), ("IQ3_S", 256, 110), ("IQ3_XXS", 256, 98),
@@ -105,3 +105,17 @@ def test_shared_expert_entry_points_check_their_arguments():
     assert ms(q, 1, 4, 4096, 1536, 1, 70000, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # > 65535 pairs
     assert ms(q, 1, 4, 4096, 1500, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # not whole blocks
     assert ms(99, 1, 4, 4096, 1536, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_KIND
+
+
+def test_router_route_checks_its_arguments():
+    lib = _lib.library()
+    rr = lib.strata_router_route
+    #        w rows cols x tokens dtype logits experts k idx weights extra count stream
+    assert rr(1, 257, 4096, 1, 9, 1, 1, 256, 8, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # more than 8 tokens
+    assert rr(1, 257, 4096, 1, 1, 1, 1, 258, 8, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # more experts than rows
+    assert rr(1, 257, 4096, 1, 1, 1, 1, 256, 65, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # k past 64
+    assert rr(1, 257, 4100, 1, 1, 1, 1, 256, 8, 1, 1, 1, 1, None) == _lib.ERR_SHAPE  # cols not a multiple of 8
+    assert rr(1, 257, 4096, 1, 1, 2, 1, 256, 8, 1, 1, 1, 1, None) == _lib.ERR_DTYPE  # bfloat16 x
+    assert rr(1, 257, 4096, 1, 1, 1, 1, 256, 8, 1, 1, 1, 0, None) == _lib.ERR_ARG  # no count
+    assert rr(0, 257, 4096, 1, 1, 1, 1, 256, 8, 1, 1, 1, 1, None) == _lib.ERR_ARG  # null weights
+    assert rr(1, 257, 4096, 1, 0, 1, 1, 256, 8, 1, 1, 1, 1, None) == _lib.OK  # no tokens
