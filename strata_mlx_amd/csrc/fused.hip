@@ -234,8 +234,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void router_route_kernel(const f1
   if (last == 0u) return;
   asm volatile("" ::: "memory");  // the logits are read after the count
   const int nx = rows - experts;
-  // the rows past the experts' (at most 256 values a thread's share of them here), then each token's choice; all of
-  // a thread's loads in flight together
+  // the rows past the experts' (tokens x nx values, two a thread a pass), then each token's choice (a wave a token);
+  // all of a thread's loads of a pass in flight together
   constexpr int kExtra = 2;  // extra values a thread per pass
   for (int i0 = 0; extra != nullptr && i0 < tokens * nx; i0 += 64 * kRouteWaves * kExtra) {
     float e[kExtra];
