@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--no-prompt", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline, decode_t4, roofline and prompt")
     ap.add_argument("--dense", action="store_true", help="only the dense half of a mixed-model decode token")
-    ap.add_argument("--only", choices=("prompt", "prompt_q2_0", "prefill", "q4k"),
+    ap.add_argument("--only", choices=("prompt", "prompt_q2_0", "prefill", "q4k", "moe"),
                     help="only this sub-workload, printed as its own line (for profiling one kernel family)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 512 MiB with torch's copy kernel three times: the known-size reference that "
@@ -348,10 +348,11 @@ def shared_down_bench(B, D, synth, dev, lins, steps, warmup, rng):
 
 
 def moe_block_bench(B, D, FU, synth, dev, lins, steps, warmup):
-    """One decode token through the layers' whole MoE blocks (fused.RoutedMoE: the router (256 x 4096 float16), its
-    top-8 and softmax, the routed IQ3_S experts, a Q4_K shared expert riding in the routed launches, its sigmoid gate,
-    the combine), each block's routing made by its own router from the same token: microseconds a block and the
-    block's bytes (the distinct experts' rows, the shared expert, the router and gate weights) over that time."""
+    """One decode token through the layers' whole MoE blocks (fused.RoutedMoE: the router (256 x 4096 float16) and
+    the shared expert's gate in one launch, the top-8 and softmax in the routed gate/up launch, the routed IQ3_S
+    experts, a Q4_K shared expert riding in the routed launches, its sigmoid gate, the combine), each block's routing
+    made by its own router from the same token: microseconds a block and the block's bytes (the distinct experts'
+    rows, the shared expert, the router and gate weights) over that time."""
     g = torch.Generator(device=dev)
     g.manual_seed(8)
     x = (torch.randn((1, H), device=dev) / 64).half()
@@ -375,8 +376,8 @@ def moe_block_bench(B, D, FU, synth, dev, lins, steps, warmup):
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     paths = sorted({moe.last_path for moe in blocks})
-    if paths != ["riding"]:
-        raise RuntimeError(f"the shared expert did not ride in the routed launches: {paths}")
+    if paths != ["choice in the launch"]:
+        raise RuntimeError(f"the choice and the shared expert were not in the routed launches: {paths}")
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         run()
@@ -390,7 +391,8 @@ def moe_block_bench(B, D, FU, synth, dev, lins, steps, warmup):
     shared_bytes = sum(lay.blocks.numel() for lay in mats[0][1])
     total = routed + shared_bytes + E * H * 2 + H * 2 + K * F * 2 + H * 2
     return {"workload": f"one decode token through {len(blocks)} MoE blocks: router 256 x 4096 float16, top-8, "
-                        f"routed IQ3_S {F} x {H} / {H} x {F}, shared expert Q4_K riding in the routed launches, "
+                        f"routed IQ3_S {F} x {H} / {H} x {F} choosing its experts in the gate/up launch, shared expert "
+                        f"Q4_K riding in the routed launches, "
                         f"its gate, the combine", "us_per_block": round(us, 2),
             "bytes_per_block": int(total), "gbs": round(total / (us * 1e-6) / 1e9, 1),
             "hbm_frac": round(total / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -569,6 +571,11 @@ def main():
             out = prompt_bench(B, synth, dev, steps, 2, rng, kind="Q2_0" if args.only == "prompt_q2_0" else "IQ3_XXS")
         elif args.only == "q4k":
             out = q4k_bench(B, synth, dev, max(2, args.steps // 5), 2)
+        elif args.only == "moe":
+            from strata_mlx_amd import dense as D
+            from strata_mlx_amd import fused as FU
+            out = moe_block_bench(B, D, FU, synth, dev, decode_layers(B, synth, dev, args.layers), args.steps,
+                                  args.warmup)
         else:
             from strata_mlx_amd import dense as D
             out = prefill_bench(B, D, synth, dev, decode_layers(B, synth, dev, 2), steps, 2, rng)

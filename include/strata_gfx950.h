@@ -87,6 +87,23 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
                                         int64_t shared_rows, void* shared_h, void* shared_g, void* shared_u,
                                         void* stream);
 
+/* strata_expert_gate_up_swiglu_shared with the pairs' experts chosen in the launch: logits (logit_rows float32,
+ * the router's products for one token: the `experts` experts' first, then any rows past them, such as a shared
+ * expert's gate), pairs = k, the top k of the experts' logits and their softmax (as strata_top_k chooses them:
+ * ties to the lower index) written to idx_out (k) and w_out (k) for the down and combine calls, and the rows past
+ * the experts' rounded to float16 into extra_out (logit_rows - experts, or NULL). out_h and shared_h as
+ * strata_expert_gate_up_swiglu_shared gives them; a logit that is NaN is never chosen, and a pair left without an
+ * expert gets index 0xffffffff and NaN in out_h. experts <= 256, k <= 64; the routed stacks IQ3_S or Q2_0 of 4096
+ * inputs at three units a wave (on 256 CUs, IQ3_S 3 to 8 pairs of 1536 rows, Q2_0 6 to 8); other cases return
+ * STRATA_ERR_SHAPE (the choice then from strata_router_route). No counterpart in the reference, whose MoE block calls the router, top_k and the
+ * experts apart (strata_mlx/fused.py:488-493): the launch's workgroups make the choice while their codebooks
+ * fill, which spares the router's launch its choice. */
+int strata_moe_gate_up_swiglu_shared(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts,
+                                     int64_t rows, int64_t cols, const float* logits, int64_t logit_rows,
+                                     int64_t pairs, const void* x, int x_dtype, void* out_h, uint32_t* idx_out,
+                                     float* w_out, int shared_kind, const void* shared_gate, const void* shared_up,
+                                     int64_t shared_rows, void* shared_h, void* extra_out, void* stream);
+
 /* strata_expert_matvec at one token (each pair's own x, share 1: the down call of a routed layer) with a shared
  * expert's down in the same launch: shared_out[r] = shared_blocks[r, :] . shared_x, shared_blocks a Q4_K matrix of
  * shared_rows x cols, shared_x its token (float16, its h), shared_out float16. The routed stack IQ3_S or Q2_0 of

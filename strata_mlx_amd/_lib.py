@@ -46,6 +46,8 @@ SIGNATURES = {
                                                  _p, _i64, _p, _p, _p, _p]),
     "strata_expert_matvec_shared": (_i, [_i, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _i, _p, _i64, _p, _p, _p]),
     "strata_router_route": (_i, [_p, _i64, _i64, _p, _i64, _i, _p, _i64, _i64, _p, _p, _p, _p, _p]),
+    "strata_moe_gate_up_swiglu_shared": (_i, [_i, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i, _p, _p, _p, _i, _p,
+                                              _p, _i64, _p, _p, _p]),
     "strata_expert_layer_workspace": (_i64, [_i64, _i64]),
     "strata_expert_layer": (_i, [_i, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i, _p, _p, _p, _i64, _p]),
     "strata_expert_matvec_swiglu": (_i, [_i, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _i, _p, _p]),

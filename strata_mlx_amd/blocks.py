@@ -181,6 +181,44 @@ def gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: tor
     return (g, u, h, sh, *sgu) if with_shared_gu else (g, u, h, sh)
 
 
+def moe_gate_up_swiglu_shared(gate: BlockSwitchLinear, up: BlockSwitchLinear, x: torch.Tensor, logits: torch.Tensor,
+                              experts: int, k: int, shared_gate, shared_up):
+    """gate_up_swiglu_shared at one token with the experts chosen in the launch from the router's float32 logits
+    (1, rows >= experts: the experts' first, then rows such as the shared expert's gate), the choice top_k makes:
+    (h (k, rows), idx (k,) int32, w (k,) float32 the softmax of the chosen logits, the shared expert's h (1, rows),
+    the logits past the experts' as float16 (1, rows - experts) or None), or None where the launch does not take
+    the case (then route_gated and gate_up_swiglu_shared). strata_mlx/fused.py:488-493 with blocks.py:969-975."""
+    if (gate.kind, gate.output_dims, gate.input_dims, gate.num_experts) != (up.kind, up.output_dims, up.input_dims,
+                                                                             up.num_experts):
+        raise ValueError("gate and up differ in type or shape")
+    if (shared_gate.kind, shared_gate.output_dims, shared_gate.input_dims) != (
+            shared_up.kind, shared_up.output_dims, shared_up.input_dims) or shared_gate.input_dims != gate.input_dims:
+        raise ValueError("the shared expert's gate and up differ in type or shape from each other or the token")
+    if getattr(shared_gate, "blocks", None) is None or getattr(shared_up, "blocks", None) is None or \
+            getattr(shared_gate, "to_file", None) is not None or getattr(shared_up, "to_file", None) is not None:
+        raise ValueError("the shared expert's layers as the file's blocks, inputs in the file's order")
+    x2 = x.reshape(-1, gate.input_dims).contiguous()
+    lg = logits.reshape(-1).contiguous()
+    if x2.shape[0] != 1 or lg.dtype != torch.float32 or lg.numel() < experts or experts != gate.num_experts:
+        return None
+    dev = x.device
+    h = torch.empty((k, gate.output_dims), dtype=x.dtype, device=dev)
+    idx = torch.empty(k, dtype=torch.int32, device=dev)
+    w = torch.empty(k, dtype=torch.float32, device=dev)
+    sh = torch.empty((1, shared_gate.output_dims), dtype=x.dtype, device=dev)
+    nx = lg.numel() - experts
+    extra = torch.empty((1, nx), dtype=torch.float16, device=dev) if nx > 0 else None
+    rc = _lib.library().strata_moe_gate_up_swiglu_shared(
+        _lib.kind_id(gate.kind), gate.blocks.data_ptr(), up.blocks.data_ptr(), gate.num_experts, gate.output_dims,
+        gate.input_dims, lg.data_ptr(), lg.numel(), k, x2.data_ptr(), _lib.dtype_id(x.dtype), h.data_ptr(),
+        idx.data_ptr(), w.data_ptr(), _lib.kind_id(shared_gate.kind), shared_gate.blocks.data_ptr(),
+        shared_up.blocks.data_ptr(), shared_gate.output_dims, sh.data_ptr(), _lib.ptr(extra), _lib.stream())
+    if rc in (_lib.ERR_SHAPE, _lib.ERR_DTYPE, _lib.ERR_KIND):
+        return None
+    _lib.check(rc, f"gate/up with the choice and the shared expert {gate.kind} + {shared_gate.kind}")
+    return h, idx, w, sh, extra
+
+
 def expert_matvec_shared(lin: BlockSwitchLinear, idx: torch.Tensor, shared):
     """The down call of one token's routed experts, out[pair] = W[idx[pair]] . x[pair] (x (pairs, in), each pair
     its own h), with a shared expert's down (a layer of the file's Q4_K blocks with `blocks`, `kind`,

@@ -142,9 +142,60 @@ int expert_common(int kind, const void* a, const void* b, int64_t experts, int64
 
 }  // namespace
 
+// The routed gate/up launch at one token with a shared expert's gate and up in it, the pairs' experts given (idx)
+// or chosen in the launch from the router's logits (logits not null: idx is then where the choice goes).
+static int gate_up_shared(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts, int64_t rows,
+                          int64_t cols, const uint32_t* idx, int64_t pairs, const void* x, int x_dtype,
+                          void* out_gate, void* out_up, void* out_h, int shared_kind, const void* shared_gate,
+                          const void* shared_up, int64_t shared_rows, void* shared_h, void* shared_g, void* shared_u,
+                          const float* logits, int64_t logit_rows, int64_t route_experts, uint32_t* idx_out,
+                          float* w_out, void* extra_out, void* stream) {
+  MatvecParams p = {};
+  int rc = block_shape(kind, rows, cols, &p.row_bytes);
+  if (rc) return rc;
+  int s_row_bytes = 0;
+  rc = block_shape(shared_kind, shared_rows, cols, &s_row_bytes);
+  if (rc) return rc;
+  if (x_dtype != DT_F16) return STRATA_ERR_DTYPE;
+  if (pairs < 1 || experts < 1 || experts > INT32_MAX || shared_rows < 1) return STRATA_ERR_ARG;
+  if (rows == 0) return STRATA_ERR_SHAPE;  // no routed launch to carry the shared expert: the two calls apart
+  if (!gate_blocks || !up_blocks || !idx || !x || !out_h || !shared_gate || !shared_up || !shared_h)
+    return STRATA_ERR_ARG;
+  if (shared_kind != K_Q4_K || pairs > 65535 || shared_rows > INT32_MAX / 2) return STRATA_ERR_SHAPE;
+  p.blocks[0] = (const uint8_t*)gate_blocks;
+  p.blocks[1] = (const uint8_t*)up_blocks;
+  p.out[0] = out_gate;
+  p.out[1] = out_up;
+  p.glu_out = out_h;
+  p.idx = idx;
+  p.x = x;
+  p.mat_bytes = rows * (int64_t)p.row_bytes;
+  p.experts = experts;
+  p.src_rows = (int)rows;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.pairs = (int)pairs;
+  p.share = (int)pairs;  // one token
+  p.mode = MODE_EXPERT;
+  p.shared[0] = (const uint8_t*)shared_gate;
+  p.shared[1] = (const uint8_t*)shared_up;
+  p.shared_out = shared_h;
+  p.shared_gu[0] = shared_g;
+  p.shared_gu[1] = shared_u;
+  p.shared_rows = (int)shared_rows;
+  p.shared_row_bytes = s_row_bytes;
+  p.route_logits = logits;
+  p.route_idx = idx_out;
+  p.route_w = w_out;
+  p.route_extra = extra_out;
+  p.route_rows = (int)logit_rows;
+  p.route_experts = (int)route_experts;
+  return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 2, (hipStream_t)stream);
+}
+
 extern "C" {
 
-int strata_abi_version(void) { return 5; }
+int strata_abi_version(void) { return 6; }
 
 int strata_block_info(int kind, int* per_block, int* block_bytes) {
   return strata_kind_info(kind, per_block, block_bytes) ? STRATA_ERR_KIND : STRATA_OK;
@@ -194,41 +245,22 @@ int strata_expert_gate_up_swiglu_shared(int kind, const void* gate_blocks, const
                                         int shared_kind, const void* shared_gate, const void* shared_up,
                                         int64_t shared_rows, void* shared_h, void* shared_g, void* shared_u,
                                         void* stream) {
-  MatvecParams p = {};
-  int rc = block_shape(kind, rows, cols, &p.row_bytes);
-  if (rc) return rc;
-  int s_row_bytes = 0;
-  rc = block_shape(shared_kind, shared_rows, cols, &s_row_bytes);
-  if (rc) return rc;
-  if (x_dtype != DT_F16) return STRATA_ERR_DTYPE;
-  if (pairs < 1 || experts < 1 || experts > INT32_MAX || shared_rows < 1) return STRATA_ERR_ARG;
-  if (rows == 0) return STRATA_ERR_SHAPE;  // no routed launch to carry the shared expert: the two calls apart
-  if (!gate_blocks || !up_blocks || !idx || !x || !out_h || !shared_gate || !shared_up || !shared_h)
-    return STRATA_ERR_ARG;
-  if (shared_kind != K_Q4_K || pairs > 65535 || shared_rows > INT32_MAX / 2) return STRATA_ERR_SHAPE;
-  p.blocks[0] = (const uint8_t*)gate_blocks;
-  p.blocks[1] = (const uint8_t*)up_blocks;
-  p.out[0] = out_gate;
-  p.out[1] = out_up;
-  p.glu_out = out_h;
-  p.idx = idx;
-  p.x = x;
-  p.mat_bytes = rows * (int64_t)p.row_bytes;
-  p.experts = experts;
-  p.src_rows = (int)rows;
-  p.rows = (int)rows;
-  p.cols = (int)cols;
-  p.pairs = (int)pairs;
-  p.share = (int)pairs;  // one token
-  p.mode = MODE_EXPERT;
-  p.shared[0] = (const uint8_t*)shared_gate;
-  p.shared[1] = (const uint8_t*)shared_up;
-  p.shared_out = shared_h;
-  p.shared_gu[0] = shared_g;
-  p.shared_gu[1] = shared_u;
-  p.shared_rows = (int)shared_rows;
-  p.shared_row_bytes = s_row_bytes;
-  return launch_by_kind(kind, p, x_dtype, x_dtype, false, (int)pairs, 2, (hipStream_t)stream);
+  if (!idx) return STRATA_ERR_ARG;
+  return gate_up_shared(kind, gate_blocks, up_blocks, experts, rows, cols, idx, pairs, x, x_dtype, out_gate, out_up,
+                        out_h, shared_kind, shared_gate, shared_up, shared_rows, shared_h, shared_g, shared_u, nullptr,
+                        0, 0, nullptr, nullptr, nullptr, stream);
+}
+
+int strata_moe_gate_up_swiglu_shared(int kind, const void* gate_blocks, const void* up_blocks, int64_t experts,
+                                     int64_t rows, int64_t cols, const float* logits, int64_t logit_rows,
+                                     int64_t pairs, const void* x, int x_dtype, void* out_h, uint32_t* idx_out,
+                                     float* w_out, int shared_kind, const void* shared_gate, const void* shared_up,
+                                     int64_t shared_rows, void* shared_h, void* extra_out, void* stream) {
+  if (!logits || !idx_out || !w_out) return STRATA_ERR_ARG;
+  if (logit_rows < experts || experts > 256 || pairs > 64 || pairs > experts) return STRATA_ERR_SHAPE;
+  return gate_up_shared(kind, gate_blocks, up_blocks, experts, rows, cols, idx_out, pairs, x, x_dtype, nullptr,
+                        nullptr, out_h, shared_kind, shared_gate, shared_up, shared_rows, shared_h, nullptr, nullptr,
+                        logits, logit_rows, experts, idx_out, w_out, extra_out, stream);
 }
 
 int strata_expert_matvec_shared(int kind, const void* blocks, int64_t experts, int64_t rows, int64_t cols,

@@ -51,6 +51,13 @@ struct MatvecParams {
   void* shared_gu[2];  // the shared expert's gate . x and up . x, or null
   const void* shared_x;  // the shared expert's token in the routed down launch (its h)
   int shared_rows, shared_row_bytes;
+  // the choice of experts made in the routed gate/up launch (one token): the router's logits (route_rows float32,
+  // the experts' route_experts first), the choice out (idx, weights) and the rows past the experts' as float16
+  const float* route_logits;
+  uint32_t* route_idx;
+  float* route_w;
+  void* route_extra;
+  int route_rows, route_experts;
 };
 
 // Copy [src, src + len) to LDS at dst + (src & 15), 16-byte loads for the aligned middle.

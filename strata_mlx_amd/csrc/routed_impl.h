@@ -35,6 +35,8 @@
 // once a pair. Q2_0 takes the same kernels with a 256-entry table of a code byte's four weights (c - 1) in place
 // of the codebook, and d for a lane's block.
 #pragma once
+
+#include "topk.h"
 // Included by direct_impl.h ahead of the dispatch (it uses that file's fields, offsets and reductions).
 
 namespace strata_mv {
@@ -292,6 +294,15 @@ struct GluParams {
   f16* s_g;  // the shared expert's gate . x, or null
   f16* s_u;  // its up . x, or null
   int s_rows, s_row_bytes;
+  // the choice of experts in the launch (routed_glu_kernel's ROUTE form, one token): the router's logits (float32,
+  // r_rows of them: the experts' r_experts first, then rows such as a shared expert's gate), the pairs' experts and
+  // weights out (idx is the launch's own choice: top `pairs` of the experts' logits, their softmax) and the rows
+  // past the experts' rounded to float16 (or null)
+  const float* r_logits;
+  uint32_t* r_idx;
+  float* r_w;
+  f16* r_extra;
+  int r_rows, r_experts;
 };
 
 // A token's piece c (16 bytes: columns 8 c .. 8 c + 7) in LDS: slot c with its low three bits XORed with the
@@ -327,7 +338,10 @@ __device__ __forceinline__ void glu_unit(typename Routed<KIND>::Fields (&f)[2], 
   up = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
-template <int KIND, int UPW, int MODE, bool SHARED = false>
+// ROUTE (one token, 256 experts at most): the pairs' experts are chosen in the launch from the router's logits, by
+// wave 0 of every workgroup while the table and the token go to LDS (the same choice as top_k's); workgroup 0 writes
+// it out for the down and combine launches. It spares the router's launch the count and the choice at its end.
+template <int KIND, int UPW, int MODE, bool SHARED = false, bool ROUTE = false>
 __global__ __launch_bounds__((glu_threads<KIND, MODE>()), (glu_threads<KIND, MODE>() / 256)) void routed_glu_kernel(
     GluParams p) {
   constexpr int kGluThreads = glu_threads<KIND, MODE>(), kGluWaves = kGluThreads / 64;
@@ -352,6 +366,16 @@ __global__ __launch_bounds__((glu_threads<KIND, MODE>()), (glu_threads<KIND, MOD
   // what the workgroup shares, asked for first: the table entry this thread expands and pieces of the tokens
   // (ONE32: quarters of float32 pieces, four values each: 1024 of them over the workgroup)
   const uint64_t entry = R::fetch(tid);
+  static_assert(!ROUTE || MODE == GLU1, "the choice in the launch: one token");
+  __shared__ uint32_t route_idx[ROUTE ? 64 : 1];
+  __shared__ float route_w[ROUTE ? 64 : 1];
+  float route_v[4];  // ROUTE: wave 0's logits, lane l holding experts l, l + 64, l + 128, l + 192
+  if constexpr (ROUTE) {
+    if (tid < 64) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) route_v[i] = p.r_logits[min(i * 64 + lane, p.r_experts - 1)];
+    }
+  }
   constexpr int kPieceLoads = MODE == ONE32 ? 1024 / kGluThreads : (512 * kTokens + kGluThreads - 1) / kGluThreads;
   u32x4 xpiece[kPieceLoads];
 #pragma unroll
@@ -388,7 +412,7 @@ __global__ __launch_bounds__((glu_threads<KIND, MODE>()), (glu_threads<KIND, MOD
   bool bad[UPW];
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
-    if constexpr (kOne) {
+    if constexpr (kOne || ROUTE) {  // ROUTE: the experts are known after the workgroup barrier below
       bad[k] = false;
       expert[k] = 0u;
     } else {
@@ -467,10 +491,34 @@ __global__ __launch_bounds__((glu_threads<KIND, MODE>()), (glu_threads<KIND, MOD
       xs[(c >> 9) * 512 + x_piece_slot(c & 511)] = xpiece[k];
     }
   }
+  if constexpr (ROUTE) {  // wave 0: the top `pairs` experts and their softmax, into LDS; workgroup 0's out as well
+    if (tid < 64) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i * 64 + lane >= p.r_experts) route_v[i] = -INFINITY;
+      strata_topk::top_k_row<4>(route_v, p.r_experts, p.pairs, lane, route_idx, route_w);
+      if (blockIdx.x == 0) {
+        if (lane < p.pairs) {
+          p.r_idx[lane] = route_idx[lane];
+          p.r_w[lane] = route_w[lane];
+        }
+        for (int e = lane; p.r_extra != nullptr && e < p.r_rows - p.r_experts; e += 64)
+          p.r_extra[e] = from_f32<f16>(p.r_logits[p.r_experts + e]);
+      }
+    }
+  }
   if constexpr (kEarlyRows)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   else
     __syncthreads();
+  if constexpr (ROUTE) {  // a row of NaN logits chooses no expert (index 0xffffffff): read as a pair naming none
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+      const uint32_t e = route_idx[pair[k]];
+      bad[k] = e >= p.experts;
+      expert[k] = bad[k] ? 0u : e;
+    }
+  }
   // lane j's activations: the 32 columns of each of its two runs
   uint32_t x[32], x2[MODE == ONE32 ? 32 : 1];
   auto read_x = [&](int t, uint32_t* dst) {
@@ -870,6 +918,26 @@ int launch_glu_mode(GluParams& p, hipStream_t s) {
   return launch_glu_upw<KIND, MODE, SHARED>(p, upw, dim3((unsigned)(waves / kWaves)), s);
 }
 
+// The ROUTE form: the one-token shared form at three units a wave (eight pairs of 1536 rows), the choice of experts
+// in the launch; other shapes return STRATA_ERR_SHAPE (the router's choice then comes from its own launch).
+template <int KIND>
+int launch_glu_route(GluParams& p, hipStream_t s) {
+  const int64_t units = (int64_t)p.na * p.nb;
+  constexpr int kWaves = glu_threads<KIND, GLU1>() / 64;
+  if (glu_units_a_wave<KIND, GLU1>(units) != 3 || p.pairs > 64 || p.r_experts > 256 || p.r_experts < p.pairs ||
+      p.r_rows < p.r_experts)
+    return STRATA_ERR_SHAPE;
+  const int64_t waves = ((units + 2) / 3 + kWaves - 1) / kWaves * kWaves;
+  p.waves = (int)waves;
+  p.wave_a = p.waves / p.nb;
+  p.wave_b = p.waves % p.nb;
+  if (p.s_rows > p.waves) return STRATA_ERR_SHAPE;  // one shared unit a wave at most
+  hipLaunchKernelGGL((routed_glu_kernel<KIND, 3, GLU1, true, true>), dim3((unsigned)(waves / kWaves)),
+                     dim3(glu_threads<KIND, GLU1>()), 0, s, p);
+  STRATA_CHECK_LAUNCH();
+  return STRATA_OK;
+}
+
 template <int KIND>
 int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
   if constexpr (!routed_kind(KIND)) {
@@ -892,6 +960,14 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
     p.tokens = mp.pairs / mp.share;
     if (mp.shared[0] != nullptr) {  // the shared expert's gate and up in the same launch: one token
       if (p.tokens != 1 || mp.shared_rows < 1) return STRATA_ERR_SHAPE;
+      if (mp.route_logits != nullptr) {  // and the choice of experts
+        p.r_logits = mp.route_logits;
+        p.r_idx = mp.route_idx;
+        p.r_w = mp.route_w;
+        p.r_extra = reinterpret_cast<f16*>(mp.route_extra);
+        p.r_rows = mp.route_rows;
+        p.r_experts = mp.route_experts;
+      }
       p.s_gate = mp.shared[0];
       p.s_up = mp.shared[1];
       p.s_h = reinterpret_cast<f16*>(mp.shared_out);
@@ -901,6 +977,7 @@ int launch_routed_glu(const MatvecParams& mp, hipStream_t s) {
       p.s_row_bytes = mp.shared_row_bytes;
       p.na = p.pairs;
       p.nb = p.rows;
+      if (mp.route_logits != nullptr) return launch_glu_route<KIND>(p, s);
       return launch_glu_mode<KIND, GLU1, true>(p, s);
     }
     if (p.tokens > 1) {

@@ -130,9 +130,11 @@ class RoutedMoE:
     file's blocks); then moe_combine(y, w, g, s), or where it declines, sum_k y_k * w_k in float32 rounded to x's
     type, plus sigmoid(g) * s, in float32 as MLX promotes it.
 
-    At one token the shared expert's gate and up ride in the routed gate/up launch and its down in the routed down
-    launch (blocks.gate_up_swiglu_shared, blocks.expert_matvec_shared), where those take the case; elsewhere, and
-    where they decline, the routed experts and the shared expert run apart. `last_path` says which ran."""
+    At one token the router's rows and the shared expert's gate go through one launch (their products), the routed
+    gate/up launch makes the choice of experts from those logits and takes the shared expert's gate and up with its
+    own rows (blocks.moe_gate_up_swiglu_shared), and the routed down launch takes the shared expert's down
+    (blocks.expert_matvec_shared): four launches with the combine. Where a launch declines, the choice comes from
+    the router's own launch (route_gated) or the calls run apart. `last_path` says which ran."""
 
     def __init__(self, router: WindowLinear, switch, shared_gate, shared_up, shared_down,
                  shared_expert_gate: WindowLinear, k: int):
@@ -151,15 +153,27 @@ class RoutedMoE:
         _, _, h = dense.gate_up_swiglu(self.shared_gate, self.shared_up, x)
         return self.shared_down(h)
 
-    def _riding(self, x: torch.Tensor, idx: torch.Tensor):
-        """(y (1, k, hidden), s (1, hidden)) with the shared expert in the routed launches, or None."""
+    def _routed_choice(self, x: torch.Tensor):
+        """At one token: the router's products (the stacked weight), then the gate/up launch that makes the choice
+        of experts itself: (y (1, k, hidden), s (1, hidden), idx, w, g) or None."""
         from . import blocks
+        if self.stacked is None or x.shape[0] != 1 or not self.stacked.takes(x):
+            return None
         sw = self.switch
-        flat = idx.reshape(-1)
-        r = blocks.gate_up_swiglu_shared(sw.gate_proj, sw.up_proj, x, flat, self.shared_gate, self.shared_up)
+        logits = self.stacked(x)
+        r = blocks.moe_gate_up_swiglu_shared(sw.gate_proj, sw.up_proj, x, logits, self.router.rows, self.k,
+                                             self.shared_gate, self.shared_up)
         if r is None:
             return None
-        _, _, h, sh = r
+        h, idx, w, sh, g = r
+        y, s = self._down(idx, h, sh)
+        self.last_path = "choice in the launch" + ("" if self.last_path == "riding" else ", shared down apart")
+        return y, s, idx.reshape(1, self.k), w.reshape(1, self.k), g
+
+    def _down(self, flat: torch.Tensor, h: torch.Tensor, sh: torch.Tensor):
+        """The routed down with the shared expert's down in it where the launch takes it: (y (1, k, hidden), s)."""
+        from . import blocks
+        sw = self.switch
         both = blocks.expert_matvec_shared(sw.down_proj, flat, self.shared_down)(h, sh)
         if both is None:  # the down launch does not take it: the shared down on its own launch
             y, s = blocks.expert_matvec(sw.down_proj, flat, h), self.shared_down(sh)
@@ -169,21 +183,36 @@ class RoutedMoE:
             self.last_path = "riding"
         return y.reshape(1, self.k, -1), s
 
+    def _riding(self, x: torch.Tensor, idx: torch.Tensor):
+        """(y (1, k, hidden), s (1, hidden)) with the shared expert in the routed launches, or None."""
+        from . import blocks
+        sw = self.switch
+        flat = idx.reshape(-1)
+        r = blocks.gate_up_swiglu_shared(sw.gate_proj, sw.up_proj, x, flat, self.shared_gate, self.shared_up)
+        if r is None:
+            return None
+        _, _, h, sh = r
+        return self._down(flat, h, sh)
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         lead, hidden = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, hidden)
-        both_gates = route_gated(self.stacked, x2, self.router.rows, self.k) if self.stacked is not None else None
-        if both_gates is None:
-            idx, w = route(self.router, x2, self.k)
-            g = self.shared_expert_gate(x2)
+        fused = self._routed_choice(x2)
+        if fused is not None:
+            y, s, idx, w, g = fused
         else:
-            idx, w, g = both_gates
-        both = self._riding(x2, idx) if x2.shape[0] == 1 else None
-        if both is None:
-            y, s = self.switch(x2, idx).reshape(x2.shape[0], self.k, -1), self.shared_expert(x2)
-            self.last_path = "apart"
-        else:
-            y, s = both
+            both_gates = route_gated(self.stacked, x2, self.router.rows, self.k) if self.stacked is not None else None
+            if both_gates is None:
+                idx, w = route(self.router, x2, self.k)
+                g = self.shared_expert_gate(x2)
+            else:
+                idx, w, g = both_gates
+            both = self._riding(x2, idx) if x2.shape[0] == 1 else None
+            if both is None:
+                y, s = self.switch(x2, idx).reshape(x2.shape[0], self.k, -1), self.shared_expert(x2)
+                self.last_path = "apart"
+            else:
+                y, s = both
         out = moe_combine(y, w, g, s)
         if out is None:
             out = (y.float() * w[..., None]).sum(dim=-2).to(x.dtype).float() + torch.sigmoid(g.float()) * s.float()

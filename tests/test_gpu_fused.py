@@ -104,7 +104,7 @@ def test_moe_block_against_the_oracle(gpu, tokens):
     xs = torch.from_numpy(x).to(gpu)
     out = moe(xs)
     assert out.shape == (tokens, H) and out.dtype == (torch.float16 if tokens <= FU.COMBINE_UPTO else torch.float32)
-    assert moe.last_path == ("riding" if tokens == 1 else "apart")
+    assert moe.last_path == ("choice in the launch" if tokens == 1 else "apart")
     idx_t, w_t = FU.route(router, xs, K)
     idx, w = idx_t.cpu().numpy(), w_t.cpu().numpy()
     got = out.float().cpu().numpy()
@@ -171,3 +171,54 @@ def test_router_and_choice_in_one_launch(gpu, tokens, experts, extra, k, dtype):
         FU.route_gated(stacked, xs[(r + 1) % 3], experts, k)  # eager work between the replays
         torch.cuda.synchronize()
     assert FU.route_gated(stacked, torch.cat([xs[0]] * 9)[:9], experts, k) is None  # 9 tokens: the calls apart
+
+
+# The routed gate/up launch that makes the choice of experts itself from the router's logits
+# (strata_moe_gate_up_swiglu_shared) against the calls it replaces, top_k on the logits then the gate/up launch with
+# the shared expert: the same experts, the weights', h's and the shared expert's h's bits, the rows past the experts
+# rounded once to float16. Logits with ties, -inf, and NaN (never chosen; a row of NaN chooses no expert, as top_k,
+# and h is then NaN); calls in a row; a shape the form does not take (ten pairs) declines.
+@pytest.mark.parametrize("kind,experts,extra,k", [("IQ3_S", 256, 1, 8), ("IQ3_S", 10, 1, 8), ("IQ3_S", 64, 0, 6),
+                                                  ("Q2_0", 256, 1, 8), ("IQ3_S", 256, 1, 10)])
+def test_gate_up_with_the_choice_in_the_launch(gpu, kind, experts, extra, k):
+    from strata_mlx_amd import blocks as B
+    from strata_mlx_amd import dense as D
+    from strata_mlx_amd import synth
+    F, H = 1536, 4096
+    g = torch.Generator(device=gpu).manual_seed(experts * 7 + k)
+    gate, up = (B.BlockSwitchLinear(synth.random_stack(kind, experts * F * H, gpu, g), kind, (experts, F, H))
+                for _ in range(2))
+    sg, su = (D.BlockLinear(synth.random_stack("Q4_K", F * H, gpu, g), "Q4_K", (F, H)) for _ in range(2))
+    rng = np.random.default_rng(experts + k)
+    n = experts + extra
+    cases = [rng.standard_normal(n).astype(np.float32) for _ in range(2)]
+    tied = np.round(rng.standard_normal(n), 1).astype(np.float32)  # many ties
+    odd = rng.standard_normal(n).astype(np.float32)
+    odd[::3] = np.nan
+    odd[1::7] = -np.inf
+    cases += [tied, odd, np.full(n, np.nan, np.float32)]
+    x = torch.from_numpy((rng.standard_normal((1, H)) / 64).astype(np.float16)).to(gpu)
+
+    def same(a, b):  # the same bits, or NaN at both
+        bits = a.view(torch.int16 if a.dtype == torch.float16 else torch.int32)
+        want = b.view(bits.dtype)
+        return bool(((bits == want) | (torch.isnan(a) & torch.isnan(b))).all())
+
+    for lg in cases:
+        logits = torch.from_numpy(lg).reshape(1, n).to(gpu)
+        got = B.moe_gate_up_swiglu_shared(gate, up, x, logits, experts, k, sg, su)
+        if k > 8:
+            assert got is None
+            return
+        h, idx, w, sh, ex = got
+        want_idx, want_w = FU.top_k(logits[:, :experts].contiguous(), k, weights=True)
+        assert torch.equal(idx, want_idx.reshape(k))
+        assert same(w, want_w.reshape(k))
+        _, _, want_h, want_sh = B.gate_up_swiglu_shared(gate, up, x, want_idx.reshape(k), sg, su)
+        assert same(h, want_h) and torch.equal(sh.view(torch.int16), want_sh.view(torch.int16))
+        if extra:
+            assert same(ex, logits[:, experts:].to(torch.float16))
+        else:
+            assert ex is None
+        if np.isnan(lg[:experts]).all():
+            assert torch.isnan(h).all() and not torch.isnan(sh).any()

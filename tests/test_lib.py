@@ -25,7 +25,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.strata_abi_version() == 5
+    assert lib.strata_abi_version() == 6
 
 
 @pytest.mark.parametrize("kind, per, size", [("Q2_0", 64, 18), ("IQ3_S", 256, 110), ("IQ3_XXS", 256, 98),
@@ -105,6 +105,18 @@ def test_shared_expert_entry_points_check_their_arguments():
     assert ms(q, 1, 4, 4096, 1536, 1, 70000, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # > 65535 pairs
     assert ms(q, 1, 4, 4096, 1500, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_SHAPE  # not whole blocks
     assert ms(99, 1, 4, 4096, 1536, 1, 8, 1, 1, 1, k4, 1, 4096, 1, 1, None) == _lib.ERR_KIND
+    mg = lib.strata_moe_gate_up_swiglu_shared
+    #        kind gate up experts rows cols logits l_rows pairs x dtype h idx w s_kind s_gate s_up s_rows s_h extra stream
+    assert mg(q, 1, 1, 256, 1536, 4096, 0, 257, 8, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_ARG  # logits
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 257, 8, 1, 1, 1, 0, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_ARG  # no idx
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 257, 8, 1, 1, 1, 1, 0, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_ARG  # no w
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 255, 8, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_SHAPE
+    assert mg(q, 1, 1, 257, 1536, 4096, 1, 257, 8, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_SHAPE
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 257, 65, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_SHAPE
+    assert mg(q, 1, 1, 4, 1536, 4096, 1, 5, 8, 1, 1, 1, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_SHAPE  # k > n
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 257, 8, 1, 0, 1, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_DTYPE
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 257, 8, 1, 1, 1, 1, 1, q, 1, 1, 1536, 1, 1, None) == _lib.ERR_SHAPE
+    assert mg(q, 1, 1, 256, 1536, 4096, 1, 257, 8, 1, 1, 0, 1, 1, k4, 1, 1, 1536, 1, 1, None) == _lib.ERR_ARG  # no h
 
 
 def test_router_route_checks_its_arguments():
