@@ -1,6 +1,7 @@
 // One block type's instances of the prompt kernels; compiled once per type with -DSTRATA_KIND=<GGUF type id>.
 #include "gemm_impl.h"
 #include "prompt_impl.h"
+#include "prompt_wide.h"
 
 #ifndef STRATA_KIND
 #error "STRATA_KIND must name a GGUF type id"
@@ -41,13 +42,13 @@ namespace strata_prompt {
 int STRATA_CAT(prompt_launch_, STRATA_KIND)(PromptParams& p, int mode, int out_dtype, hipStream_t s) {
   if constexpr (strata_mv::FastTraits<STRATA_KIND>::supported) {
     if (mode == PM_GLU) {
-      if (out_dtype == DT_F16) return launch_prompt<STRATA_KIND, PM_GLU, f16>(p, s);
-      if (out_dtype == DT_BF16) return launch_prompt<STRATA_KIND, PM_GLU, bf16_t>(p, s);
+      if (out_dtype == DT_F16) return launch_prompt_split<STRATA_KIND, PM_GLU, f16>(p, s);
+      if (out_dtype == DT_BF16) return launch_prompt_split<STRATA_KIND, PM_GLU, bf16_t>(p, s);
       return STRATA_ERR_DTYPE;
     }
     if (mode == PM_SCATTER) {
-      if (out_dtype == DT_F16) return launch_prompt<STRATA_KIND, PM_SCATTER, f16>(p, s);
-      if (out_dtype == DT_BF16) return launch_prompt<STRATA_KIND, PM_SCATTER, bf16_t>(p, s);
+      if (out_dtype == DT_F16) return launch_prompt_split<STRATA_KIND, PM_SCATTER, f16>(p, s);
+      if (out_dtype == DT_BF16) return launch_prompt_split<STRATA_KIND, PM_SCATTER, bf16_t>(p, s);
       return STRATA_ERR_DTYPE;
     }
     return STRATA_ERR_ARG;

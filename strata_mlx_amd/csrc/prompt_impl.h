@@ -56,7 +56,10 @@ struct PromptParams {
   void* out;                    // C32: float (slots x rows); SwiGLU: h (slots x rows); scatter: y (pairs x rows)
   int64_t experts, mat_bytes;
   int rows, cols, row_bytes, n_tiles, row_blocks;
+  int skip_full;  // the full chunks of kFullChunk tiles are another launch's (prompt_wide.h): take the runs' tails
 };
+
+constexpr int kFullChunk = 16;  // tiles of a full chunk, taken by prompt_wide.h when PromptParams.skip_full is set
 
 // The run's own scale, as a float16 pair: IQ3_S 1 + 2s, IQ3_XXS 2s + 1, Q2_0 d.
 template <int KIND>
@@ -678,6 +681,11 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
     }
     before += seen;
     more = seen == 256;
+  }
+  if (p.skip_full) {  // a run's first floor(L / 16) * 16 tiles are full chunks, another launch's; the tail is this one's
+    const int run0 = t0 - before, probe = run0 + kFullChunk * (before / kFullChunk + 1) - 1;
+    if (probe < p.n_tiles && p.tile_expert[probe] == e) return;  // the run goes on past t0's block of 16: full
+    before %= kFullChunk;                                          // the tail's tiles before t0
   }
   if (__builtin_amdgcn_readfirstlane(before) % NT != 0) return;  // a tile of a chunk that starts before it
   int nt = 1;

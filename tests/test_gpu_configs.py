@@ -389,3 +389,35 @@ def test_bfloat16_prompt_outside_float16s_range(gpu):
     for rows in (slice(0, None, 3), slice(1, None, 3), slice(2, None, 3)):  # each scale of rows on its own
         sel = np.arange(len(flat)).reshape(tokens, k)[rows].reshape(-1)
         assert rel_l2(y[sel], want[sel]) <= REL
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "IQ3_XXS", "Q2_0"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prompt_full_chunks_and_tails(gpu, kind, dtype):
+    """A long prompt over few experts, eight tiles an expert or more: each expert's run of tiles split into full
+    chunks of 16 (the wide form, an expert's rows decoded once a step for all 16 tiles) and a tail of 0 to 15 tiles
+    (the chunked form), through switch_glu's tiles: gate/up 512 x 768 (three steps), down 768 x 512, 16 experts
+    picked with weights 1 .. 16 (runs of about 4 to 30 tiles), 1024 tokens top-4, against the oracle's chain."""
+    experts, rows, cols, tokens, k = 16, 512, 768, 1024, 4
+    layer = {n: Stack(kind, experts, r, c, 940 + i, gpu) for i, (n, (r, c)) in
+             enumerate((("gate", (rows, cols)), ("up", (rows, cols)), ("down", (cols, rows))))}
+    rng = np.random.default_rng(17)
+    weights = np.arange(1, experts + 1, dtype=np.float64)
+    idx = np.stack([rng.choice(experts, k, replace=False, p=weights / weights.sum()) for _ in range(tokens)])
+    tiles = -(-np.bincount(idx.reshape(-1), minlength=experts) // 16)
+    assert tiles.sum() >= 8 * experts and (tiles >= 16).sum() >= 4 and len(set(tiles % 16)) >= 6
+    x = (rng.standard_normal((tokens, cols)) / 16).astype(np.float32)
+    xs, ix = torch.from_numpy(x).to(dtype).to(gpu), torch.from_numpy(idx.astype(np.int32)).to(gpu)
+    y = B.BlockSwitchGLU(layer["gate"].lin, layer["up"].lin, layer["down"].lin)(xs, ix)
+    y = y.float().cpu().numpy().reshape(-1, cols)
+    flat = idx.reshape(-1)
+    xr = xs.float().cpu().numpy().astype(np.float64)
+    want = np.empty((len(flat), cols))
+    for e in np.unique(flat):
+        at = np.nonzero(flat == e)[0]
+        g = xr[at // k] @ layer["gate"].weights(e).astype(np.float64).T
+        u = xr[at // k] @ layer["up"].weights(e).astype(np.float64).T
+        h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+        h = torch.from_numpy(h).to(dtype).float().numpy().astype(np.float64)  # the SwiGLU rounded to the type
+        want[at] = h @ layer["down"].weights(e).astype(np.float64).T
+    assert rel_l2(y, as_dtype(want, dtype)) <= REL
