@@ -683,9 +683,11 @@ __global__ __launch_bounds__(64 * WAVES, kMinWaves) void prompt_kernel(PromptPar
     more = seen == 256;
   }
   if (p.skip_full) {  // a run's first floor(L / 16) * 16 tiles are full chunks, another launch's; the tail is this one's
-    const int run0 = t0 - before, probe = run0 + kFullChunk * (before / kFullChunk + 1) - 1;
-    if (probe < p.n_tiles && p.tile_expert[probe] == e) return;  // the run goes on past t0's block of 16: full
-    before %= kFullChunk;                                          // the tail's tiles before t0
+    // t0's block of 16 from the run's first tile is full if every tile from t0 to its end names e (lanes 0-15)
+    const int left = kFullChunk - before % kFullChunk, t = t0 + (tid & 63);
+    const bool ok = (tid & 63) >= left || (t < p.n_tiles && p.tile_expert[t] == e);
+    if (__ballot(!ok) == 0) return;  // a full chunk's tile
+    before %= kFullChunk;            // the tail's tiles before t0
   }
   if (__builtin_amdgcn_readfirstlane(before) % NT != 0) return;  // a tile of a chunk that starts before it
   int nt = 1;

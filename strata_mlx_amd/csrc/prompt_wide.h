@@ -78,8 +78,9 @@ __device__ __forceinline__ int wide_scan(int v, int* scratch, int tid, int& tota
 }
 
 // The full chunks' first tiles, in order, into chunks; returns their number. A chunk starts at every tile whose
-// offset from its run's first tile (a run: consecutive tiles of one expert) is a multiple of kWideChunk and whose
-// run goes on for kWideChunk tiles from it; tiles naming no expert make none. Thread t looks at tiles 20 t .. 20 t + 19.
+// offset from its run's first tile (a run: consecutive tiles of one expert, wherever they lie: an expert may have
+// several) is a multiple of kWideChunk and whose run goes on for kWideChunk tiles from it; tiles naming no expert
+// make none. Thread t looks at tiles 20 t .. 20 t + 19.
 __device__ __forceinline__ int wide_plan(const PromptParams& p, uint16_t* chunks, int* scratch, int tid) {
   constexpr int kPer = kWideMaxTiles / kWideThreads;
   static_assert(kPer * kWideThreads == kWideMaxTiles, "whole tiles a thread");
@@ -111,9 +112,11 @@ __device__ __forceinline__ int wide_plan(const PromptParams& p, uint16_t* chunks
       if (i < n) {
         if (i == 0 || tv[k] != pv) r = i;
         pv = tv[k];
-        if ((uint64_t)tv[k] < (uint64_t)p.experts && (i - r) % kWideChunk == 0 && i + kWideChunk - 1 < n &&
-            p.tile_expert[i + kWideChunk - 1] == tv[k])
-          at(i);
+        if ((uint64_t)tv[k] < (uint64_t)p.experts && (i - r) % kWideChunk == 0 && i + kWideChunk - 1 < n) {
+          bool full = true;  // every tile of the block names the run's expert (a run: contiguous tiles of one)
+          for (int j = 1; j < kWideChunk && full; ++j) full = p.tile_expert[i + j] == tv[k];
+          if (full) at(i);
+        }
       }
     }
   };

@@ -421,3 +421,58 @@ def test_prompt_full_chunks_and_tails(gpu, kind, dtype):
         h = torch.from_numpy(h).to(dtype).float().numpy().astype(np.float64)  # the SwiGLU rounded to the type
         want[at] = h @ layer["down"].weights(e).astype(np.float64).T
     assert rel_l2(y, as_dtype(want, dtype)) <= REL
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "Q2_0"])
+def test_prompt_split_with_an_expert_in_two_runs(gpu, kind):
+    """The C ABI's tiles in any order (strata_prompt_gate_up_swiglu, strata_prompt_down: every slot of a tile naming
+    an expert, whatever the tiles around it), with the full-chunk split on (eight tiles an expert or more): expert 0
+    in two runs (20 tiles, then 17 after another expert's 3), expert 2 in a run of exactly 16, short runs, and
+    tiles naming no expert, whose rows of h stay as they were. h and y against the oracle's chain at 1e-3."""
+    from strata_mlx_amd import _lib
+    experts, rows, cols, n_tok = 4, 512, 768, 64
+    runs = [(0, 20), (1, 3), (0, 17), (2, 16), (3, 2), (experts, 2)]
+    te = np.concatenate([np.full(n, e, np.uint32) for e, n in runs])
+    n_tiles = len(te)
+    assert n_tiles >= 8 * experts
+    layer = {n: Stack(kind, experts, r, c, 960 + i, gpu) for i, (n, (r, c)) in
+             enumerate((("gate", (rows, cols)), ("up", (rows, cols)), ("down", (cols, rows))))}
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((n_tok, cols)) / 16).astype(np.float16)
+    slots = n_tiles * 16
+    token = rng.integers(0, n_tok, slots).astype(np.uint32)
+    e_slot = np.repeat(te, 16)
+    filled = e_slot < experts
+    pairs = int(filled.sum())
+    slot_pair = np.full(slots, 0xFFFFFFFF, np.uint32)
+    slot_pair[filled] = rng.permutation(pairs).astype(np.uint32)
+    idx = np.empty(pairs, np.uint32)
+    idx[slot_pair[filled]] = e_slot[filled]
+    d = lambda a: torch.from_numpy(a).to(gpu)
+    xs, tok, tes, sp, ix = d(x), d(token.view(np.int32)), d(te.view(np.int32)), d(slot_pair.view(np.int32)), d(
+        idx.view(np.int32))
+    h = torch.full((slots, rows), 7.0, dtype=torch.float16, device=gpu)
+    y = torch.empty((pairs, cols), dtype=torch.float16, device=gpu)
+    lib, kid = _lib.library(), _lib.kind_id(kind)
+    _lib.check(lib.strata_prompt_gate_up_swiglu(kid, layer["gate"].lin.blocks.data_ptr(), layer["up"].lin.blocks.data_ptr(),
+                                                experts, rows, cols, xs.data_ptr(), None, tok.data_ptr(), tes.data_ptr(),
+                                                n_tiles, 16, h.data_ptr(), _lib.dtype_id(torch.float16), _lib.stream()),
+               "gate/up")
+    _lib.check(lib.strata_prompt_down(kid, layer["down"].lin.blocks.data_ptr(), experts, cols, rows, h.data_ptr(), None,
+                                      tes.data_ptr(), n_tiles, 16, sp.data_ptr(), ix.data_ptr(), pairs, y.data_ptr(),
+                                      _lib.dtype_id(torch.float16), _lib.stream()), "down")
+    torch.cuda.synchronize()
+    hg, yg = h.float().cpu().numpy(), y.float().cpu().numpy()
+    assert (hg[~filled] == 7.0).all()
+    xr = x.astype(np.float64)
+    h_want = np.zeros((slots, rows))
+    y_want = np.zeros((pairs, cols))
+    for e in range(experts):
+        at = np.nonzero(e_slot == e)[0]
+        g = xr[token[at]] @ layer["gate"].weights(e).astype(np.float64).T
+        u = xr[token[at]] @ layer["up"].weights(e).astype(np.float64).T
+        he = (g / (1.0 + np.exp(-g)) * u).astype(np.float32).astype(np.float16)
+        h_want[at] = he
+        y_want[slot_pair[at]] = he.astype(np.float64) @ layer["down"].weights(e).astype(np.float64).T
+    assert rel_l2(hg[filled], h_want[filled]) <= REL
+    assert rel_l2(yg, as_dtype(y_want, torch.float16)) <= REL
