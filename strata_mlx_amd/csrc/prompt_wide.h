@@ -36,9 +36,11 @@
 namespace strata_prompt {
 
 constexpr int kWideWaves = 8;                         // waves a workgroup
-constexpr int kWidePerCU = 8 / kWideWaves;            // workgroups a CU: two waves a SIMD
+constexpr int kWidePerCU = 1;                         // workgroups a CU
+constexpr int kWideWavesSimd = 2;                     // waves a SIMD the kernel is built for
 constexpr int kWideThreads = 64 * kWideWaves;
-constexpr int kWideGroups = kWideWaves;               // groups of 16 weight rows an item, one a wave
+constexpr int kWideGroups = kWideWaves;               // groups of 16 weight rows an item
+constexpr int kGroupsWave = kWideGroups / kWideWaves;  // groups a wave decodes
 constexpr int kWideTilesWave = 2;                     // tiles a wave multiplies at most
 constexpr int kWideChunk = kWideWaves * kWideTilesWave;  // tiles a chunk
 static_assert(kWideChunk == kFullChunk, "the chunked form's tails start where the full chunks end");
@@ -163,11 +165,18 @@ __device__ __forceinline__ void wide_item(const PromptParams& p, const DirectTab
                                           float* ratio, float* last, uint32_t e, int t0, int rb, int wave, int lane) {
   const int n = lane & 15, g = lane >> 4;
   constexpr bool kGlu = MODE == PM_GLU;
-  // this wave's group of rows: SwiGLU form, the first half of the groups gate rows, the second the same rows of up
+  // this wave's groups of rows, wave + kWideWaves j: SwiGLU form, the first half of the groups gate rows, the second
+  // the same rows of up
   constexpr int kHalf = kWideGroups / 2;
-  const int grow = kGlu ? rb * 16 * kHalf + 16 * (wave % kHalf) + n : rb * 16 * kWideGroups + 16 * wave + n;
-  const uint8_t* mat = (kGlu && wave >= kHalf ? p.blocks[1] : p.blocks[0]) + (int64_t)e * p.mat_bytes;
-  const uint32_t off = (uint32_t)min(grow, p.rows - 1) * (uint32_t)p.row_bytes;  // past the last row: the last
+  const uint8_t* mat[kGroupsWave];
+  uint32_t off[kGroupsWave];
+#pragma unroll
+  for (int j = 0; j < kGroupsWave; ++j) {
+    const int gi = wave + kWideWaves * j;
+    const int grow = kGlu ? rb * 16 * kHalf + 16 * (gi % kHalf) + n : rb * 16 * kWideGroups + 16 * gi + n;
+    mat[j] = (kGlu && gi >= kHalf ? p.blocks[1] : p.blocks[0]) + (int64_t)e * p.mat_bytes;
+    off[j] = (uint32_t)min(grow, p.rows - 1) * (uint32_t)p.row_bytes;  // past the last row: the last
+  }
   const LaneOffsets<KIND> o = strata_mv::lane_offsets<KIND>(g);
   const int nsteps = p.cols / kStep;
   const uint32_t step_bytes = (uint32_t)(p.row_bytes / nsteps);
@@ -180,14 +189,29 @@ __device__ __forceinline__ void wide_item(const PromptParams& p, const DirectTab
     arow[i] = p.a + (int64_t)r * p.cols;
   }
 
-  RunPair<KIND> f[2];  // f[s % 2]: step s's fields
-  strata_mv::load_fields<KIND>(mat, off, o, f[0]);
-  strata_mv::load_fields<KIND>(mat, off + (nsteps > 1 ? step_bytes : 0u), o, f[1]);
-  float s = 1.0f;  // the decoding lane's row: the step scale in force
+  RunPair<KIND> f[2][kGroupsWave];  // f[s % 2][j]: step s's fields of group j
+  float s[kGroupsWave];              // the decoding lane's rows: the step scale in force
   // ratio: [step parity][group][row]; last: [group][row], the scale in force after the last step
-  wide_decode<KIND>(f[0], g, tab, wdec + wave * 8 * 64, ratio + wave * 16, s, lane);
-  if (nsteps == 1 && g == 0) last[wave * 16 + n] = s;
-  if (nsteps > 2) strata_mv::load_fields<KIND>(mat, off + 2 * step_bytes, o, f[0]);
+  auto decode = [&](int k, int slot) {
+#pragma unroll
+    for (int j = 0; j < kGroupsWave; ++j) {
+      const int gi = wave + kWideWaves * j;
+      wide_decode<KIND>(f[slot][j], g, tab, wdec + (k & 1) * kWideBuf + gi * 8 * 64,
+                        ratio + (k & 1) * (16 * kWideGroups) + gi * 16, s[j], lane);
+      if (k + 1 == nsteps && g == 0) last[gi * 16 + n] = s[j];
+    }
+  };
+  auto fields = [&](int k, int slot) {
+#pragma unroll
+    for (int j = 0; j < kGroupsWave; ++j)
+      strata_mv::load_fields<KIND>(mat[j], off[j] + (uint32_t)k * step_bytes, o, f[slot][j]);
+  };
+#pragma unroll
+  for (int j = 0; j < kGroupsWave; ++j) s[j] = 1.0f;
+  fields(0, 0);
+  fields(nsteps > 1 ? 1 : 0, 1);
+  decode(0, 0);
+  if (nsteps > 2) fields(2, 0);
   lds_barrier();
 
   f32x4 acc[kWideGroups][NTW > 0 ? NTW : 1];
@@ -211,10 +235,8 @@ __device__ __forceinline__ void wide_item(const PromptParams& p, const DirectTab
       const int k = kb + sp;
       if (k < nsteps) {
         if (k + 1 < nsteps) {  // step k + 1 into the other buffer, then its fields' slot takes step k + 3's
-          wide_decode<KIND>(f[sp ^ 1], g, tab, wdec + ((k + 1) & 1) * kWideBuf + wave * 8 * 64,
-                            ratio + ((k + 1) & 1) * (16 * kWideGroups) + wave * 16, s, lane);
-          if (k + 2 == nsteps && g == 0) last[wave * 16 + n] = s;
-          if (k + 3 < nsteps) strata_mv::load_fields<KIND>(mat, off + (uint32_t)(k + 3) * step_bytes, o, f[sp ^ 1]);
+          decode(k + 1, sp ^ 1);
+          if (k + 3 < nsteps) fields(k + 3, sp ^ 1);
         }
         if constexpr (NTW > 0 && has_step_scale<KIND>()) {  // the sums into step k's scale
 #pragma unroll
@@ -285,8 +307,8 @@ __device__ __forceinline__ void wide_item(const PromptParams& p, const DirectTab
 }
 
 template <int KIND, int MODE, typename OT>
-__global__ __launch_bounds__(kWideThreads, 2) void prompt_wide_kernel(PromptParams p) {
-  static_assert(kWideGroups == kWideWaves && kWideGroups % 2 == 0, "one group of rows a wave");
+__global__ __launch_bounds__(kWideThreads, kWideWavesSimd) void prompt_wide_kernel(PromptParams p) {
+  static_assert(kWideGroups % kWideWaves == 0 && kWideGroups % 2 == 0, "whole groups of rows a wave");
   static_assert(MODE == PM_GLU || MODE == PM_SCATTER, "the SwiGLU and scatter forms");
   __shared__ __attribute__((aligned(16))) u32x4 wdec[2 * kWideBuf];
   __shared__ DirectTables<KIND> tab;
