@@ -19,7 +19,7 @@ Beside it, on the same line, the other workloads of the path:
   dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K fused into one launch, o
                  Q8_0, the shared expert's Q4_K gate and up 1536 x 4096 with the SwiGLU in one launch and its
                  down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16 token each (graphs over copies, at least
-                 1 GB a graph); shared_in_routed: the shared expert's gate and up taken by the headline layers'
+                 1 GB and 8 copies a graph, so that a replay's start spreads over 8 launches or more); shared_in_routed: the shared expert's gate and up taken by the headline layers'
                  routed gate+up launches instead (its marginal time over those launches alone);
                  shared_down_in_routed: its down taken by the layers' routed down launches the same way
   moe_block      one decode token through whole MoE blocks (fused.RoutedMoE: router, top-8, routed experts, the
@@ -212,7 +212,7 @@ def dense_bench(B, synth, dev, steps, warmup):
     for name, kind, rows, cols, how in DENSE:
         per, bb = synth.DENSE.get(kind) or synth.BLOCK[kind]
         nbytes = rows * cols // per * bb
-        copies = max(2, -(-(1 << 30) // nbytes))
+        copies = max(8, -(-(1 << 30) // nbytes))
         mats = [synth.random_stack(kind, rows * cols, dev, g) for _ in range(copies)]
         x = (torch.randn((1, cols), device=dev) / 8).half()
         if how == "glu":  # gate: the first half of the rows, up: the second
