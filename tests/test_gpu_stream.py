@@ -1,5 +1,5 @@
 """The dense one-token matvec of a long Q6_K matrix (an lm_head), whose rows are staged in LDS by 16-byte direct
-loads (stream_rows_kernel): sampled rows are the float64 product of the oracle's weights within the window test's
+loads (stream_rows_kernel; from 65536 rows with the non-temporal cache policy): sampled rows are the float64 product of the oracle's weights within the window test's
 bound (test_dense.py:49: 4e-3 relative to the largest output), and listed rows (rows.py:30-42) have the full
 product's bits, in the order listed, repeats included, NaN for an id past the layer."""
 
@@ -13,7 +13,7 @@ from strata_mlx_amd import blocks as B
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("rows", [8192, 12288, 40037])
+@pytest.mark.parametrize("rows", [8192, 12288, 40037, 65603])
 def test_lm_head_rows_are_the_product(gpu, rows):
     rng = np.random.default_rng(rows)
     cols = 4096
