@@ -19,8 +19,9 @@ Beside it, on the same line, the other workloads of the path:
   dense_decode   the dense half of a mixed-model decode token: q, k, v 4096 x 4096 Q6_K fused into one launch, o
                  Q8_0, the shared expert's Q4_K gate and up 1536 x 4096 with the SwiGLU in one launch and its
                  down 4096 x 1536, lm_head 151936 x 4096 Q6_K, one float16 token each (graphs over copies, at least
-                 1 GB and 8 copies a graph, so that a replay's start spreads over 8 launches or more); shared_in_routed: the shared expert's gate and up taken by the headline layers'
-                 routed gate+up launches instead (its marginal time over those launches alone);
+                 1 GB and 8 copies a graph, so that a replay's start spreads over 8 launches or more);
+                 shared_in_routed: the shared expert's gate and up taken by the headline layers' routed gate+up
+                 launches instead (its marginal time over those launches alone);
                  shared_down_in_routed: its down taken by the layers' routed down launches the same way
   moe_block      one decode token through whole MoE blocks (fused.RoutedMoE: router, top-8, routed experts, the
                  shared expert riding in the routed launches, its gate, the combine): us a block and GB/s
@@ -32,7 +33,8 @@ Beside it, on the same line, the other workloads of the path:
                  host's cores) on a few layers of the headline workload; q4k_matvec carries its own
 
 --dense prints only dense_decode as its own line; --only NAME one other sub-workload (prompt, prompt_q2_0, prefill
-with two IQ3_S layers, q4k).
+with two IQ3_S layers, q4k); --prefill-tokens N the prefill's prompt length (2048; at 4096 and more, eight tiles
+an expert or more, the experts' full chunks of 16 tiles take the wide form).
 """
 
 import argparse
@@ -60,6 +62,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prompt", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline, decode_t4, roofline and prompt")
@@ -493,9 +496,9 @@ def q4k_bench(B, synth, dev, steps, warmup, copies=64):
 
 
 def prefill_bench(B, D, synth, dev, lins, steps, warmup, rng, tokens=2048):
-    """A 2048-token prefill of the mixed model, bfloat16: the routed IQ3_S experts of `lins` (Zipf top-8) through
-    the tiles, and the dense layers (q, k, v Q6_K fused, o Q8_0, the shared expert's Q4_K gate and up fused, down) as
-    the reference multiplies a prompt chunk: each dequantized for the chunk, then the library product. Returns
+    """A prefill of `tokens` tokens (2048 by default) of the mixed model, bfloat16: the routed IQ3_S experts of `lins`
+    (Zipf top-8) through the tiles, and the dense layers (q, k, v Q6_K fused, o Q8_0, the shared expert's Q4_K gate
+    and up fused, down) as the reference multiplies a prompt chunk: each dequantized for the chunk, then the library product. Returns
     TFLOPS over the real products' flops, each part and all."""
     g = torch.Generator(device=dev)
     g.manual_seed(4)
@@ -531,7 +534,7 @@ def prefill_bench(B, D, synth, dev, lins, steps, warmup, rng, tokens=2048):
     ms = out["routed"]["ms"] / len(lins) + out["dense"]["ms"]
     for v in out.values():
         v.pop("_flops")
-    out.update({"workload": "2048-token prefill, bf16: routed IQ3_S 256 experts top-8 (one layer) + dense q/k/v "
+    out.update({"workload": f"{tokens}-token prefill, bf16: routed IQ3_S 256 experts top-8 (one layer) + dense q/k/v "
                             "Q6_K, o Q8_0, shared expert Q4_K", "tflops": round(fl / ms / 1e9, 2),
                 "ms_per_layer": round(ms, 4), "mfma_peak_frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)})
     return out
@@ -578,7 +581,8 @@ def main():
                                   args.warmup)
         else:
             from strata_mlx_amd import dense as D
-            out = prefill_bench(B, D, synth, dev, decode_layers(B, synth, dev, 2), steps, 2, rng)
+            out = prefill_bench(B, D, synth, dev, decode_layers(B, synth, dev, 2), steps, 2, rng,
+                                tokens=args.prefill_tokens)
         print(json.dumps({args.only: out}))
         return
     note(f"making {args.layers} IQ3_S layers of 256 experts")
@@ -653,7 +657,8 @@ def main():
         from strata_mlx_amd import fused as FU
         result["moe_block"] = moe_block_bench(B, D, FU, synth, dev, lins, args.steps, args.warmup)
         note("2048-token prefill")
-        result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng)
+        result["prefill"] = prefill_bench(B, D, synth, dev, lins[:2], max(2, args.steps // 10), 2, rng,
+                                          tokens=args.prefill_tokens)
     if not args.no_cpu_baseline:
         note("cpu baseline")
         layers, done, secs, threads = cpu_baseline(lins, routes, args.tokens)
