@@ -39,7 +39,8 @@ def test_top_k_chooses_as_a_stable_sort_and_weights_by_softmax(gpu, n, k):
     np.testing.assert_allclose(wts.cpu().numpy(), OF.softmax_k(logits, want), rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("rows,k,d", [(1, 8, 4096), (4, 8, 4096), (16, 10, 512), (3, 20, 256)])
+@pytest.mark.parametrize("rows,k,d", [(1, 8, 4096), (4, 8, 4096), (2, 4, 1024), (5, 6, 768), (16, 10, 512),
+                                      (3, 20, 256)])
 def test_combine_has_the_references_bits(gpu, rows, k, d):
     rng = np.random.default_rng(rows * k)
     y = (rng.standard_normal((rows, k, d)) * 4).astype(np.float16)
